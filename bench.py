@@ -1,0 +1,185 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused causal attention path on one MI355X.
+
+Workload (the metric's shape): causal scaled-dot-product
+attention forward + backward, fp32 I/O, B=1, H=12, S=4096, D=64, Q/K/V/dO iid
+N(0,1) from fixed seeds, scale 1/8. One step = dfattn_fwd (O, lse) followed by
+dfattn_bwd (its two phases: preprocess, main) on inputs already resident in HBM.
+
+FLOPs follow the reference's convention (darkforest-core/src/bin/bench_sequence_limit.rs:226):
+causal forward = 2*H*S^2*D, backward = 2.5x forward, so one step = 7*H*S^2*D
+= 90.19 GFLOP.
+
+Prints ONE JSON line. `roofline` is for the dominant kernel (the one with the
+largest average duration, timed live with HIP events on the stream the
+library launches on); `cpu_baseline` times the CPU oracle (a restatement of
+the reference's fp32 CPU attention) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dark-forest_amd"))
+
+import numpy as np  # noqa: E402
+
+H, S, D = 12, 4096, 64
+SCALE = 1.0 / 8.0
+FLOP_FWD = 2.0 * H * S * S * D
+FLOP_BWD = 2.5 * FLOP_FWD
+FLOP_STEP = FLOP_FWD + FLOP_BWD
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+SEED = 3000
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def seeded(seq_len, n_heads, d_head, seed):
+    dm = n_heads * d_head
+    return [np.random.Generator(np.random.PCG64(seed + i)).standard_normal((seq_len, dm), dtype=np.float32)
+            for i in range(4)]
+
+
+def cpu_baseline(heads: int):
+    """The CPU oracle (oracle/attention_oracle.c), 1 thread, on `heads` of the 12 heads."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    q, k, v, g = seeded(S, H, D, SEED)
+    cols = slice(0, heads * D)
+    q, k, v, g = (np.ascontiguousarray(a[:, cols]) for a in (q, k, v, g))
+    t0 = time.perf_counter()
+    O.mha_forward(q, k, v, heads, SCALE, True, threads=1)
+    O.backward(q, k, v, g, heads, SCALE, True, threads=1)
+    dt = time.perf_counter() - t0
+    flops = FLOP_STEP * heads / H
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"heads 0..{heads - 1} of {H} at S={S}, D={D}: causal fwd+bwd, fp32, 1 thread "
+                      f"({dt:.1f} s; {flops / 1e9:.2f} GFLOP algorithmic)",
+            "seconds": round(dt, 3)}
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-heads", type=int, default=4, help="heads in the CPU baseline sample (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import dfattn
+
+    dev = torch.device("cuda:0")
+    log(f"library: {dfattn.version()}  device: {torch.cuda.get_device_name(0)}")
+    q, k, v, g = (torch.from_numpy(a).to(dev) for a in seeded(S, H, D, SEED))
+    o = torch.empty_like(q)
+    lse = torch.empty((H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ws = torch.empty(dfattn.bwd_workspace_bytes(H, S, D) // 4, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        dfattn.attention_forward(q, k, v, H, SCALE, True, out=o, lse=lse)
+        if ev is not None:
+            ev[1].record(stream)
+        dfattn.backward_preprocess(o, g, dq, ws, H)
+        if ev is not None:
+            ev[2].record(stream)
+        dfattn.backward_main(q, k, v, g, lse, dq, dk, dv, ws, H, SCALE, True)
+        if ev is not None:
+            ev[3].record(stream)
+
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
+    pre_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
+    main_ms = float(np.mean([e[2].elapsed_time(e[3]) for e in events]))
+    step_ev_ms = sorted(e[0].elapsed_time(e[3]) for e in events)
+    log(f"fwd {fwd_ms:.4f} ms, bwd preprocess {pre_ms:.4f} ms, bwd main {main_ms:.4f} ms, wall/step {ms_per_step:.4f} ms")
+
+    kernels = {
+        "fwd_d64_kernel": (fwd_ms, FLOP_FWD),
+        "bwd_main_kernel": (main_ms, FLOP_BWD),
+    }
+    name, (kms, kflop) = max(kernels.items(), key=lambda kv: kv[1][0])
+    achieved = kflop / (kms * 1e-3) / 1e12
+    traffic = load_traffic()
+    roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved, 2), "peak": PEAK_F16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16_TFLOPS, 4),
+                "traffic": (traffic or {}).get(name, {}).get("hbm_bytes_per_launch"),
+                "avg_launch_ms": round(kms, 5)}
+
+    value = FLOP_STEP / (ms_per_step * 1e-3) / 1e12
+    result = {
+        "metric": "causal attn fwd+bwd TFLOP/s (S=4096,H=12,D=64) + % MFMA peak; GPT-2 step ms",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA operands, f32 accumulate/softmax, f32 I/O",
+        "data": "synthetic: Q,K,V,dO iid N(0,1), PCG64 seeds 3000..3003",
+        "config": {"workload": "C2 causal SDPA fwd+bwd (BASELINE configs[2])", "B": 1, "H": H, "S": S, "D": D,
+                   "scale": SCALE, "io": "fp32", "flop_per_step": FLOP_STEP},
+        "pct_mfma_peak": round(100 * value / PEAK_F16_TFLOPS, 2),
+        "fwd_ms": round(fwd_ms, 5),
+        "bwd_ms": round(pre_ms + main_ms, 5),
+        "bwd_preprocess_ms": round(pre_ms, 5),
+        "fwd_tflops": round(FLOP_FWD / (fwd_ms * 1e-3) / 1e12, 2),
+        "bwd_tflops": round(FLOP_BWD / ((pre_ms + main_ms) * 1e-3) / 1e12, 2),
+        "step_event_ms_median": round(step_ev_ms[len(step_ev_ms) // 2], 5),
+        "step_event_ms_min": round(step_ev_ms[0], 5),
+        "roofline": roofline,
+        "gpt2_step_ms": None,
+    }
+    if args.cpu_heads > 0:
+        log(f"cpu baseline on {args.cpu_heads} heads")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,289 @@
+// dfattn_api.hip — the C ABI of include/dfattn.h: argument validation,
+// kernel selection, the reference's launcher symbols and the error state.
+//
+// Kernel selection: d_head == 64 with 16-byte aligned tensors takes the MFMA
+// kernels (attn_fwd_d64.hip, attn_bwd_d64.hip); every other valid shape takes
+// the exact fp32 kernels in attn_generic.hip. There is no CPU path.
+#include <climits>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <string>
+
+#include "dfattn.h"
+#include "dfattn_internal.h"
+
+namespace {
+
+std::mutex g_err_mu;
+int g_err = DFATTN_OK;
+std::string g_err_msg;
+
+int record_error(int status, const std::string &msg) {
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  g_err = status;
+  g_err_msg = msg;
+  return status;
+}
+
+int record_hip(hipError_t err, const char *where) {
+  if (err == hipSuccess) return DFATTN_OK;
+  return record_error(DFATTN_ERR_HIP, std::string(where) + ": " + hipGetErrorString(err));
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Shape checks shared by every entry point (the reference's are in
+// AttentionContext::new_shared, darkforest-cuda/src/lib.rs:1981-1989).
+int check_shape(const char *fn, uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
+  if (n_heads == 0 || seq_len == 0)
+    return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": n_heads and seq_len must be >= 1");
+  if (d_head == 0 || d_head > 128)
+    return record_error(DFATTN_ERR_HEAD_DIM, std::string(fn) + ": d_head must be in the range 1..=128");
+  size_t dm = 0, elems = 0, bytes = 0;
+  if (__builtin_mul_overflow((size_t)n_heads, (size_t)d_head, &dm) ||
+      __builtin_mul_overflow((size_t)seq_len, dm, &elems) ||
+      __builtin_mul_overflow(elems, sizeof(float), &bytes) || seq_len > (1u << 30) ||
+      n_heads > (1u << 20))
+    return record_error(DFATTN_ERR_OVERFLOW, std::string(fn) + ": attention shape is too large");
+  return DFATTN_OK;
+}
+
+int check_ptrs(const char *fn, std::initializer_list<const void *> ptrs) {
+  for (const void *p : ptrs) {
+    if (p == nullptr)
+      return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null tensor pointer");
+    if (!aligned(p, alignof(float)))
+      return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": tensor pointer not 4-byte aligned");
+  }
+  return DFATTN_OK;
+}
+
+bool fast_path(uint32_t d_head, std::initializer_list<const void *> ptrs) {
+  if (d_head != 64) return false;
+  for (const void *p : ptrs)
+    if (p != nullptr && !aligned(p, 16)) return false;
+  return true;
+}
+
+int fwd_impl(const float *q, const float *k, const float *v, float *o, float *lse,
+             uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal,
+             hipStream_t stream) {
+  hipError_t err;
+  if (fast_path(d_head, {q, k, v, o, lse}))
+    err = dfattn::launch_fwd_d64(q, k, v, o, lse, (int)n_heads, (int)seq_len, scale, causal != 0,
+                                 stream);
+  else
+    err = dfattn::launch_fwd_generic(q, k, v, o, lse, (int)n_heads, (int)seq_len, (int)d_head,
+                                     scale, causal != 0, stream);
+  return record_hip(err, "attention forward launch");
+}
+
+// Legacy backward: the caller's probability scratch (`capacity` floats) holds
+// O, lse and the fast path's workspace when it is large enough; otherwise the
+// self-contained generic kernel runs.
+void legacy_backward(const char *fn, const float *q, const float *k, const float *v,
+                     const float *d_out, float *d_q, float *d_k, float *d_v, float *scratch,
+                     size_t capacity, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                     float scale, uint32_t causal) {
+  if (check_shape(fn, n_heads, seq_len, d_head) != DFATTN_OK) return;
+  if (check_ptrs(fn, {q, k, v, d_out, d_q, d_k, d_v}) != DFATTN_OK) return;
+  const size_t elems = (size_t)seq_len * n_heads * d_head;
+  const size_t lse_floats = ((size_t)n_heads * seq_len + 63) / 64 * 64;
+  const size_t ws_floats = dfattn::bwd_workspace_bytes_d64((int)n_heads, (int)seq_len) / sizeof(float);
+  const bool fits = scratch != nullptr && elems + lse_floats + ws_floats <= capacity;
+  hipError_t err;
+  if (fits && fast_path(d_head, {q, k, v, d_out, d_q, d_k, d_v, scratch})) {
+    float *o_ws = scratch;
+    float *lse_ws = scratch + elems;
+    float *bwd_ws = lse_ws + lse_floats;
+    err = dfattn::launch_fwd_d64(q, k, v, o_ws, lse_ws, (int)n_heads, (int)seq_len, scale,
+                                 causal != 0, nullptr);
+    if (err == hipSuccess)
+      err = dfattn::launch_bwd_d64(q, k, v, o_ws, d_out, lse_ws, d_q, d_k, d_v, bwd_ws,
+                                   (int)n_heads, (int)seq_len, scale, causal != 0, nullptr);
+  } else {
+    err = dfattn::launch_bwd_generic(q, k, v, d_out, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
+                                     (int)d_head, scale, causal != 0, nullptr);
+  }
+  record_hip(err, fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- reference launcher symbols ------------------------------------------
+
+void launch_fused_attention(const float *q, const float *k, const float *v, float *out,
+                            uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal) {
+  const char *fn = "launch_fused_attention";
+  if (check_shape(fn, 1, seq_len, d_head) != DFATTN_OK) return;
+  if (check_ptrs(fn, {q, k, v, out}) != DFATTN_OK) return;
+  fwd_impl(q, k, v, out, nullptr, 1, seq_len, d_head, scale, causal, nullptr);
+}
+
+void launch_fused_mha_forward(const float *q, const float *k, const float *v, float *out,
+                              uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale,
+                              uint32_t causal) {
+  const char *fn = "launch_fused_mha_forward";
+  if (check_shape(fn, n_heads, seq_len, d_head) != DFATTN_OK) return;
+  if (check_ptrs(fn, {q, k, v, out}) != DFATTN_OK) return;
+  fwd_impl(q, k, v, out, nullptr, n_heads, seq_len, d_head, scale, causal, nullptr);
+}
+
+void launch_attention_backward(const float *q, const float *k, const float *v,
+                               const float *d_out, float *d_q, float *d_k, float *d_v,
+                               float *probabilities, uint32_t seq_len, uint32_t d_head,
+                               float scale, uint32_t causal) {
+  // Scratch is [seq_len, seq_len] (lib.rs:2441).
+  legacy_backward("launch_attention_backward", q, k, v, d_out, d_q, d_k, d_v, probabilities,
+                  (size_t)seq_len * seq_len, 1, seq_len, d_head, scale, causal);
+}
+
+void launch_fused_mha_backward(const float *q, const float *k, const float *v,
+                               const float *d_out, float *d_q, float *d_k, float *d_v,
+                               float *probabilities, uint32_t n_heads, uint32_t seq_len,
+                               uint32_t d_head, float scale, uint32_t causal) {
+  // Scratch is [n_heads, 2, seq_len, seq_len] (lib.rs:2023).
+  legacy_backward("launch_fused_mha_backward", q, k, v, d_out, d_q, d_k, d_v, probabilities,
+                  (size_t)n_heads * 2 * seq_len * seq_len, n_heads, seq_len, d_head, scale, causal);
+}
+
+void darkforest_sync(void) {
+  hipError_t err = hipDeviceSynchronize();
+  if (err != hipSuccess) {
+    fprintf(stderr, "[darkforest] HIP kernel error at sync boundary: %s\n", hipGetErrorString(err));
+    abort();
+  }
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  if (g_err != DFATTN_OK) {
+    fprintf(stderr, "[darkforest] attention launch error before sync boundary: %s\n",
+            g_err_msg.c_str());
+    abort();
+  }
+}
+
+// ---- fast path -------------------------------------------------------------
+
+int dfattn_fwd(const float *q, const float *k, const float *v, float *o, float *lse,
+               uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal,
+               void *stream) {
+  const char *fn = "dfattn_fwd";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o});
+  if (st == DFATTN_OK && lse != nullptr) st = check_ptrs(fn, {lse});
+  if (st != DFATTN_OK) return st;
+  return fwd_impl(q, k, v, o, lse, n_heads, seq_len, d_head, scale, causal,
+                  static_cast<hipStream_t>(stream));
+}
+
+size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
+  if (n_heads == 0 || seq_len == 0 || d_head == 0 || d_head > 128 || seq_len > (1u << 30) ||
+      n_heads > (1u << 20))
+    return 0;
+  return dfattn::bwd_workspace_bytes_d64((int)n_heads, (int)seq_len);
+}
+
+namespace {
+int check_workspace(const char *fn, const void *workspace, size_t workspace_bytes,
+                    uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
+  const size_t need = dfattn_bwd_workspace_bytes(n_heads, seq_len, d_head);
+  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, alignof(float)))
+    return record_error(DFATTN_ERR_WORKSPACE,
+                        std::string(fn) + ": workspace must be non-null, 4-byte aligned and hold " +
+                            std::to_string(need) + " bytes");
+  return DFATTN_OK;
+}
+}  // namespace
+
+int dfattn_bwd(const float *q, const float *k, const float *v, const float *o, const float *d_o,
+               const float *lse, float *d_q, float *d_k, float *d_v, void *workspace,
+               size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+               float scale, uint32_t causal, void *stream) {
+  const char *fn = "dfattn_bwd";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse, d_q, d_k, d_v});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st != DFATTN_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  if (fast_path(d_head, {q, k, v, o, d_o, lse, d_q, d_k, d_v}))
+    err = dfattn::launch_bwd_d64(q, k, v, o, d_o, lse, d_q, d_k, d_v, workspace, (int)n_heads,
+                                 (int)seq_len, scale, causal != 0, s);
+  else
+    err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
+                                     (int)d_head, scale, causal != 0, s);
+  return record_hip(err, "attention backward launch");
+}
+
+int dfattn_bwd_preprocess(const float *o, const float *d_o, float *d_q, void *workspace,
+                          size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
+                          uint32_t d_head, void *stream) {
+  const char *fn = "dfattn_bwd_preprocess";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {o, d_o, d_q});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st != DFATTN_OK) return st;
+  // The generic kernel recomputes its row statistics itself: nothing to do.
+  if (!fast_path(d_head, {o, d_o, d_q})) return DFATTN_OK;
+  return record_hip(dfattn::launch_bwd_pre_d64(o, d_o, d_q, workspace, (int)n_heads, (int)seq_len,
+                                               static_cast<hipStream_t>(stream)),
+                    "attention backward preprocess launch");
+}
+
+int dfattn_bwd_main(const float *q, const float *k, const float *v, const float *d_o,
+                    const float *lse, float *d_q, float *d_k, float *d_v, void *workspace,
+                    size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                    float scale, uint32_t causal, void *stream) {
+  const char *fn = "dfattn_bwd_main";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, d_o, lse, d_q, d_k, d_v});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st != DFATTN_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  if (fast_path(d_head, {q, k, v, d_o, lse, d_q, d_k, d_v}))
+    err = dfattn::launch_bwd_main_d64(q, k, v, d_o, lse, d_q, d_k, d_v, workspace, (int)n_heads,
+                                      (int)seq_len, scale, causal != 0, s);
+  else
+    err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
+                                     (int)d_head, scale, causal != 0, s);
+  return record_hip(err, "attention backward launch");
+}
+
+const char *dfattn_status_string(int status) {
+  switch (status) {
+    case DFATTN_OK: return "ok";
+    case DFATTN_ERR_NULL_POINTER: return "null pointer";
+    case DFATTN_ERR_MISALIGNED: return "misaligned pointer";
+    case DFATTN_ERR_SHAPE: return "invalid shape";
+    case DFATTN_ERR_HEAD_DIM: return "d_head out of range";
+    case DFATTN_ERR_OVERFLOW: return "shape overflow";
+    case DFATTN_ERR_WORKSPACE: return "workspace too small";
+    case DFATTN_ERR_HIP: return "HIP error";
+    default: return "unknown status";
+  }
+}
+
+int dfattn_last_error(void) {
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  return g_err;
+}
+
+const char *dfattn_last_error_message(void) {
+  static thread_local std::string copy;
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  copy = g_err_msg;
+  return copy.c_str();
+}
+
+void dfattn_clear_error(void) {
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  g_err = DFATTN_OK;
+  g_err_msg.clear();
+}
+
+const char *dfattn_version(void) { return "dfattn 0.1.0 (gfx950, MFMA f16 / fp32 accumulate)"; }
+
+}  // extern "C"

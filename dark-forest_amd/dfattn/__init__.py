@@ -1,0 +1,219 @@
+"""dfattn — Python binding of libdfattn.so, the gfx950 fused causal attention library.
+
+The library's C ABI is include/dfattn.h. This module loads the in-tree build
+(dark-forest_amd/lib/libdfattn.so) with ctypes and offers:
+
+* ``lib()``: the raw ctypes handle with every exported symbol typed;
+* torch-tensor wrappers over the fast path (``attention_forward``,
+  ``attention_backward``) and over the reference's launcher symbols
+  (``launch_fused_mha_forward`` ...), taking device tensors and passing their
+  pointers and torch's current HIP stream;
+* ``AttentionContext``, the mirror of the reference's per-layer context
+  (darkforest-cuda/src/lib.rs:1949-2368), and the host-slice helpers
+  ``fused_attention_forward`` / ``attention_backward`` (lib.rs:2371, 2421).
+
+There is no CPU fallback: if the library is missing every call raises
+``DfattnNotBuilt``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_PKG_DIR), "lib", "libdfattn.so")
+
+DFATTN_OK = 0
+STATUS_NAMES = {
+    0: "DFATTN_OK",
+    -1: "DFATTN_ERR_NULL_POINTER",
+    -2: "DFATTN_ERR_MISALIGNED",
+    -3: "DFATTN_ERR_SHAPE",
+    -4: "DFATTN_ERR_HEAD_DIM",
+    -5: "DFATTN_ERR_OVERFLOW",
+    -6: "DFATTN_ERR_WORKSPACE",
+    -7: "DFATTN_ERR_HIP",
+}
+
+# Every symbol include/dfattn.h declares, with (restype, argtypes).
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_F = ctypes.c_float
+SYMBOLS = {
+    "launch_fused_attention": (None, [_P, _P, _P, _P, _U32, _U32, _F, _U32]),
+    "launch_fused_mha_forward": (None, [_P, _P, _P, _P, _U32, _U32, _U32, _F, _U32]),
+    "launch_attention_backward": (None, [_P] * 8 + [_U32, _U32, _F, _U32]),
+    "launch_fused_mha_backward": (None, [_P] * 8 + [_U32, _U32, _U32, _F, _U32]),
+    "darkforest_sync": (None, []),
+    "dfattn_fwd": (ctypes.c_int, [_P] * 5 + [_U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_bwd_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
+    "dfattn_bwd": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 4 + [ctypes.c_size_t, _U32, _U32, _U32, _P]),
+    "dfattn_bwd_main": (ctypes.c_int, [_P] * 9 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "dfattn_last_error": (ctypes.c_int, []),
+    "dfattn_last_error_message": (ctypes.c_char_p, []),
+    "dfattn_clear_error": (None, []),
+    "dfattn_version": (ctypes.c_char_p, []),
+}
+
+
+class DfattnNotBuilt(RuntimeError):
+    """libdfattn.so is missing: run __graft_entry__.build() (or make -C dark-forest_amd/csrc)."""
+
+
+class DfattnError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library with typed symbols. Raises DfattnNotBuilt if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise DfattnNotBuilt(f"{LIB_PATH} not found; build it with __graft_entry__.build()")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SYMBOLS.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return handle
+
+
+def version() -> str:
+    return lib().dfattn_version().decode()
+
+
+def _check(status: int) -> None:
+    if status != DFATTN_OK:
+        msg = lib().dfattn_last_error_message().decode()
+        raise DfattnError(status, msg)
+
+
+# ---------------------------------------------------------------- torch layer
+def _torch():
+    import torch
+
+    return torch
+
+
+def _stream_ptr(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev_ptr(t):
+    if t is None:
+        return None
+    torch = _torch()
+    if not t.is_cuda:
+        raise ValueError("dfattn works on device tensors; got a CPU tensor")
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError("dfattn tensors must be contiguous float32")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _dims(q, n_heads):
+    seq_len, dm = q.shape
+    if dm % n_heads:
+        raise ValueError("q.shape[1] must be n_heads * d_head")
+    return seq_len, dm // n_heads
+
+
+def attention_forward(q, k, v, n_heads, scale=None, causal=True, out=None, lse=None, stream=None):
+    """Fast-path forward. q, k, v: [S, H*D] float32 on the GPU. Returns (O, lse[H, S])."""
+    torch = _torch()
+    seq_len, d_head = _dims(q, n_heads)
+    if scale is None:
+        scale = d_head ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty((n_heads, seq_len), dtype=torch.float32, device=q.device)
+    _check(lib().dfattn_fwd(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out), _dev_ptr(lse),
+                            n_heads, seq_len, d_head, scale, int(bool(causal)), _stream_ptr(stream)))
+    return out, lse
+
+
+def bwd_workspace_bytes(n_heads, seq_len, d_head) -> int:
+    return int(lib().dfattn_bwd_workspace_bytes(n_heads, seq_len, d_head))
+
+
+def attention_backward(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d_q=None, d_k=None,
+                       d_v=None, workspace=None, stream=None):
+    """Fast-path backward from the forward's O and lse. Returns (dQ, dK, dV)."""
+    torch = _torch()
+    seq_len, d_head = _dims(q, n_heads)
+    if scale is None:
+        scale = d_head ** -0.5
+    d_q = torch.empty_like(q) if d_q is None else d_q
+    d_k = torch.empty_like(q) if d_k is None else d_k
+    d_v = torch.empty_like(q) if d_v is None else d_v
+    need = bwd_workspace_bytes(n_heads, seq_len, d_head)
+    if workspace is None:
+        workspace = torch.empty(max(need, 4) // 4, dtype=torch.float32, device=q.device)
+    _check(lib().dfattn_bwd(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o), _dev_ptr(lse),
+                            _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(workspace),
+                            workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head, scale,
+                            int(bool(causal)), _stream_ptr(stream)))
+    return d_q, d_k, d_v
+
+
+def backward_preprocess(o, d_o, d_q, workspace, n_heads, stream=None):
+    """First phase of attention_backward (row statistics, dQ := 0)."""
+    seq_len, d_head = _dims(o, n_heads)
+    _check(lib().dfattn_bwd_preprocess(_dev_ptr(o), _dev_ptr(d_o), _dev_ptr(d_q), _dev_ptr(workspace),
+                                       workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head,
+                                       _stream_ptr(stream)))
+
+
+def backward_main(q, k, v, d_o, lse, d_q, d_k, d_v, workspace, n_heads, scale=None, causal=True, stream=None):
+    """Second phase of attention_backward (the fused dQ/dK/dV kernel)."""
+    seq_len, d_head = _dims(q, n_heads)
+    if scale is None:
+        scale = d_head ** -0.5
+    _check(lib().dfattn_bwd_main(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(d_o), _dev_ptr(lse),
+                                 _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(workspace),
+                                 workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head, scale,
+                                 int(bool(causal)), _stream_ptr(stream)))
+
+
+def launch_fused_mha_forward(q, k, v, out, n_heads, seq_len, d_head, scale, causal):
+    """The reference's launcher symbol (attention_fused.cu:233), null stream."""
+    lib().launch_fused_mha_forward(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out), n_heads, seq_len,
+                                   d_head, scale, int(bool(causal)))
+
+
+def launch_fused_attention(q, k, v, out, seq_len, d_head, scale, causal):
+    """attention_fused.cu:223, null stream."""
+    lib().launch_fused_attention(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out), seq_len, d_head, scale,
+                                 int(bool(causal)))
+
+
+def launch_fused_mha_backward(q, k, v, d_out, d_q, d_k, d_v, probabilities, n_heads, seq_len, d_head, scale,
+                              causal):
+    """attention_fused.cu:518, null stream."""
+    lib().launch_fused_mha_backward(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(d_out), _dev_ptr(d_q),
+                                    _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(probabilities), n_heads, seq_len,
+                                    d_head, scale, int(bool(causal)))
+
+
+def launch_attention_backward(q, k, v, d_out, d_q, d_k, d_v, probabilities, seq_len, d_head, scale, causal):
+    """attention_fused.cu:361, null stream."""
+    lib().launch_attention_backward(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(d_out), _dev_ptr(d_q),
+                                    _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(probabilities), seq_len, d_head,
+                                    scale, int(bool(causal)))
+
+
+def darkforest_sync():
+    """matmul.cu:21: device synchronize; aborts the process on error."""
+    lib().darkforest_sync()
+

@@ -1,0 +1,157 @@
+/*
+ * dfattn.h — C ABI of the MI355X (gfx950) fused causal attention library.
+ *
+ * This is the drop-in boundary for Dark Forest's attention path. The library
+ * (libdfattn.so) exports two groups of symbols:
+ *
+ *  1. The reference's own launcher symbols, with identical C signatures and
+ *     semantics, so a binary that linked the reference's `darkforest_kernels`
+ *     attention object links this library instead:
+ *       launch_fused_attention     darkforest-cuda/kernels/attention_fused.cu:223
+ *       launch_fused_mha_forward   darkforest-cuda/kernels/attention_fused.cu:233
+ *       launch_attention_backward  darkforest-cuda/kernels/attention_fused.cu:361
+ *       launch_fused_mha_backward  darkforest-cuda/kernels/attention_fused.cu:518
+ *       darkforest_sync            darkforest-cuda/kernels/matmul.cu:21
+ *     The Rust wrappers that bind them are darkforest-cuda/src/kernels.rs:689-885
+ *     (cuda_fused_attention, cuda_attention_backward, cuda_fused_mha_forward,
+ *     cuda_fused_mha_backward) and kernels.rs:9-20 (cuda_sync).
+ *
+ *  2. The fast path, which the reference does not have: a forward that also
+ *     writes the natural-log logsumexp of every query row, and a backward that
+ *     recomputes P from that logsumexp with an O(H*S) workspace instead of the
+ *     reference's H*2*S*S probability scratch. These take an explicit HIP
+ *     stream and return a status code; nothing aborts.
+ *
+ * Tensor layout (both groups), as in attention_fused.cu:60-66 and :404-414:
+ * every tensor is fp32, contiguous, row-major [seq_len, n_heads * d_head];
+ * head h occupies columns [h*d_head, (h+1)*d_head). Batch is 1. The
+ * single-head launchers use [seq_len, d_head]. Logsumexp is fp32 [n_heads,
+ * seq_len]: lse[h*seq_len + i] = ln sum_{j visible to i} exp(scale * q_i . k_j).
+ *
+ * `causal != 0` restricts query i to keys j <= i. `scale` multiplies q . k
+ * before the softmax (the reference's callers pass 1/sqrt(d_head)).
+ */
+#ifndef DFATTN_H
+#define DFATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Status codes of the fast-path entry points ------------------------ */
+typedef enum dfattn_status {
+  DFATTN_OK = 0,
+  DFATTN_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                 */
+  DFATTN_ERR_MISALIGNED = -2,     /* a tensor pointer is not 4-byte aligned     */
+  DFATTN_ERR_SHAPE = -3,          /* n_heads == 0 or seq_len == 0               */
+  DFATTN_ERR_HEAD_DIM = -4,       /* d_head outside 1..=128                     */
+  DFATTN_ERR_OVERFLOW = -5,       /* seq_len*n_heads*d_head does not fit        */
+  DFATTN_ERR_WORKSPACE = -6,      /* workspace NULL or smaller than required    */
+  DFATTN_ERR_HIP = -7             /* a HIP launch failed (see dfattn_last_error) */
+} dfattn_status;
+
+/* ---- Group 1: the reference's launcher symbols ---------------------------
+ * Same signatures as the reference. Launches go to the legacy default (null)
+ * stream; the functions return nothing. Argument errors that the reference
+ * would turn into a device trap (d_head > 128) or a failed launch are recorded
+ * instead and reported by darkforest_sync(), which, like the reference,
+ * prints the error and aborts.                                              */
+
+/* attention_fused.cu:223 — single-head forward, tensors [seq_len, d_head].  */
+void launch_fused_attention(const float *q, const float *k, const float *v,
+                            float *out, uint32_t seq_len, uint32_t d_head,
+                            float scale, uint32_t causal);
+
+/* attention_fused.cu:233 — multi-head forward, tensors [seq_len, H*d_head].
+ * Writes O only (the reference has no logsumexp output).                   */
+void launch_fused_mha_forward(const float *q, const float *k, const float *v,
+                              float *out, uint32_t n_heads, uint32_t seq_len,
+                              uint32_t d_head, float scale, uint32_t causal);
+
+/* attention_fused.cu:361 — single-head backward. `probabilities` is the
+ * caller's [seq_len, seq_len] fp32 scratch; it is used as workspace for O,
+ * logsumexp and row statistics when large enough. dQ, dK, dV are fully
+ * overwritten (the reference zeroes dK and dV itself, :367-369).           */
+void launch_attention_backward(const float *q, const float *k, const float *v,
+                               const float *d_out, float *d_q, float *d_k,
+                               float *d_v, float *probabilities,
+                               uint32_t seq_len, uint32_t d_head, float scale,
+                               uint32_t causal);
+
+/* attention_fused.cu:518 — multi-head backward. `probabilities` is the
+ * caller's [n_heads, 2, seq_len, seq_len] fp32 scratch (lib.rs:2023).      */
+void launch_fused_mha_backward(const float *q, const float *k, const float *v,
+                               const float *d_out, float *d_q, float *d_k,
+                               float *d_v, float *probabilities,
+                               uint32_t n_heads, uint32_t seq_len,
+                               uint32_t d_head, float scale, uint32_t causal);
+
+/* matmul.cu:21 — device synchronize; on any recorded or HIP error print
+ * "[darkforest] ..." to stderr and abort(), as the reference does.         */
+void darkforest_sync(void);
+
+/* ---- Group 2: fast path -------------------------------------------------
+ * `stream` is a hipStream_t passed as an opaque pointer (NULL = the null
+ * stream). All validation happens on the host before any HIP call; on error
+ * nothing is launched and a negative dfattn_status is returned.            */
+
+/* Forward: O [S, H*D] and lse [H, S] (lse may be NULL to skip it).
+ * No allocation: only the caller's Q, K, V, O and lse are touched.
+ * Reference counterpart: launch_fused_mha_forward (attention_fused.cu:233),
+ * plus the logsumexp output that the reference does not produce.           */
+int dfattn_fwd(const float *q, const float *k, const float *v, float *o,
+               float *lse, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+               float scale, uint32_t causal, void *stream);
+
+/* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len)
+ * (row statistics Delta_i = dO_i . O_i and a per-head dO range scale).
+ * Returns 0 when the arguments are invalid.                                */
+size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len,
+                                  uint32_t d_head);
+
+/* Backward from the forward's O and lse: writes dQ, dK, dV [S, H*D] (all
+ * fully overwritten). `workspace` must hold dfattn_bwd_workspace_bytes().
+ * Reference counterpart: launch_fused_mha_backward (attention_fused.cu:518),
+ * which recomputes the softmax from scratch with an O(S^2) buffer instead. */
+int dfattn_bwd(const float *q, const float *k, const float *v, const float *o,
+               const float *d_o, const float *lse, float *d_q, float *d_k,
+               float *d_v, void *workspace, size_t workspace_bytes,
+               uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+               float scale, uint32_t causal, void *stream);
+
+/* The two phases of dfattn_bwd, for callers that schedule or time them
+ * separately (dfattn_bwd is exactly preprocess then main, on one stream,
+ * with one workspace). Preprocess reads O and dO, writes the workspace's row
+ * statistics and zeroes dQ; main reads them and writes dQ, dK, dV. No
+ * reference counterpart: the reference backward is one kernel without
+ * saved statistics (attention_fused.cu:390-516).                            */
+int dfattn_bwd_preprocess(const float *o, const float *d_o, float *d_q,
+                          void *workspace, size_t workspace_bytes,
+                          uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                          void *stream);
+int dfattn_bwd_main(const float *q, const float *k, const float *v,
+                    const float *d_o, const float *lse, float *d_q, float *d_k,
+                    float *d_v, void *workspace, size_t workspace_bytes,
+                    uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                    float scale, uint32_t causal, void *stream);
+
+/* Human-readable name of a dfattn_status value.                             */
+const char *dfattn_status_string(int status);
+
+/* The last error recorded by any entry point of this library on any thread
+ * (0 if none), and a message for it; dfattn_clear_error() resets it.       */
+int dfattn_last_error(void);
+const char *dfattn_last_error_message(void);
+void dfattn_clear_error(void);
+
+/* Library version string and the device architecture the kernels target.   */
+const char *dfattn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFATTN_H */

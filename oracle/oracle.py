@@ -1,0 +1,162 @@
+"""numpy front end of the CPU attention oracle (oracle/attention_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
+the checker, and by bench.py's cpu_baseline leg. The product path
+(dark-forest_amd/dfattn and libdfattn.so) never imports this module.
+
+Every function takes and returns contiguous numpy arrays in the reference's
+layout: [S, H*D] for Q, K, V, O, dO, dQ, dK, dV and [H, S] for logsumexp.
+The restated reference functions are named in attention_oracle.c's header:
+static_gpt2.rs:2766-2798 (multi-head forward), lib.rs:2493-2527
+(reference_attention) and lib.rs:2529-2586 (reference_backward).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+MUTATIONS = {
+    "none": 0,
+    "causal_off_by_one": 1,
+    "drop_scale": 2,
+    "k_from_v": 3,
+    "drop_correction": 4,
+    "dk_sign": 5,
+    "head_index": 6,
+    "lse_log2": 7,
+    "dv_from_ds": 8,
+    "transpose_dq": 9,
+}
+
+
+def build() -> str:
+    """Compile liboracle.so with oracle/Makefile (gcc, no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    f32p = ctypes.POINTER(ctypes.c_float)
+    f64p = ctypes.POINTER(ctypes.c_double)
+    i64p = ctypes.POINTER(ctypes.c_int64)
+    c_int, c_float, c_double = ctypes.c_int, ctypes.c_float, ctypes.c_double
+    lib.oracle_mha_forward_f32.argtypes = [f32p, f32p, f32p, f32p, f32p, c_int, c_int, c_int, c_float, c_int, c_int]
+    lib.oracle_mha_forward_f64.argtypes = [f64p, f64p, f64p, f64p, f64p, c_int, c_int, c_int, c_double, c_int, c_int]
+    lib.oracle_mha_forward_rows_f32.argtypes = [f32p, f32p, f32p, i64p, c_int, f32p, f32p, c_int, c_int, c_int, c_float, c_int, c_int]
+    lib.oracle_reference_attention_f32.argtypes = [f32p, f32p, f32p, f32p, c_int, c_int, c_float, c_int]
+    lib.oracle_reference_backward_f32.argtypes = [f32p] * 7 + [c_int, c_int, c_int, c_float, c_int, c_int]
+    lib.oracle_backward_f64.argtypes = [f64p] * 7 + [c_int, c_int, c_int, c_double, c_int, c_int]
+    lib.oracle_set_mutation.argtypes = [c_int]
+    lib.oracle_get_mutation.restype = c_int
+    lib.oracle_max_threads.restype = c_int
+    for fn in (lib.oracle_mha_forward_f32, lib.oracle_mha_forward_f64, lib.oracle_mha_forward_rows_f32,
+               lib.oracle_reference_attention_f32, lib.oracle_reference_backward_f32, lib.oracle_backward_f64,
+               lib.oracle_set_mutation):
+        fn.restype = None
+    _lib = lib
+    return lib
+
+
+def _ptr(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _as(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def default_threads() -> int:
+    return int(_load().oracle_max_threads())
+
+
+def set_mutation(name: str) -> None:
+    """Plant a known mistake in the oracle (tests of the pinning checks only)."""
+    _load().oracle_set_mutation(MUTATIONS[name])
+
+
+def mha_forward(q, k, v, n_heads, scale, causal=True, threads=1, dtype=np.float32):
+    """Multi-head forward (static_gpt2.rs:2766-2798). Returns (O, lse)."""
+    lib = _load()
+    ct = ctypes.c_float if dtype == np.float32 else ctypes.c_double
+    q, k, v = _as(q, dtype), _as(k, dtype), _as(v, dtype)
+    seq_len, dm = q.shape
+    d_head = dm // n_heads
+    out = np.empty_like(q)
+    lse = np.empty((n_heads, seq_len), dtype=dtype)
+    fn = lib.oracle_mha_forward_f32 if dtype == np.float32 else lib.oracle_mha_forward_f64
+    fn(_ptr(q, ct), _ptr(k, ct), _ptr(v, ct), _ptr(out, ct), _ptr(lse, ct),
+       n_heads, seq_len, d_head, ct(scale), int(bool(causal)), int(threads))
+    return out, lse
+
+
+def mha_forward_rows(q, k, v, rows, n_heads, scale, causal=True, threads=1):
+    """Forward for selected query rows only. Returns (O_rows [n, H*D], lse_rows [n, H])."""
+    lib = _load()
+    q, k, v = _as(q, np.float32), _as(k, np.float32), _as(v, np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    seq_len, dm = q.shape
+    d_head = dm // n_heads
+    out = np.empty((rows.size, dm), dtype=np.float32)
+    lse = np.empty((rows.size, n_heads), dtype=np.float32)
+    lib.oracle_mha_forward_rows_f32(_ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+                                    _ptr(rows, ctypes.c_int64), int(rows.size), _ptr(out, ctypes.c_float),
+                                    _ptr(lse, ctypes.c_float), n_heads, seq_len, d_head, ctypes.c_float(scale),
+                                    int(bool(causal)), int(threads))
+    return out, lse
+
+
+def reference_attention(q, k, v, scale, causal=True):
+    """Single-head forward (lib.rs:2493-2527), tensors [S, D]."""
+    lib = _load()
+    q, k, v = _as(q, np.float32), _as(k, np.float32), _as(v, np.float32)
+    seq_len, d_head = q.shape
+    out = np.empty_like(q)
+    lib.oracle_reference_attention_f32(_ptr(q, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+                                       _ptr(out, ctypes.c_float), seq_len, d_head, ctypes.c_float(scale),
+                                       int(bool(causal)))
+    return out
+
+
+def backward(q, k, v, d_out, n_heads, scale, causal=True, threads=1, dtype=np.float32):
+    """Backward (lib.rs:2529-2586 per head). Returns (dQ, dK, dV)."""
+    lib = _load()
+    ct = ctypes.c_float if dtype == np.float32 else ctypes.c_double
+    q, k, v, d_out = (_as(a, dtype) for a in (q, k, v, d_out))
+    seq_len, dm = q.shape
+    d_head = dm // n_heads
+    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    fn = lib.oracle_reference_backward_f32 if dtype == np.float32 else lib.oracle_backward_f64
+    fn(_ptr(q, ct), _ptr(k, ct), _ptr(v, ct), _ptr(d_out, ct), _ptr(dq, ct), _ptr(dk, ct), _ptr(dv, ct),
+       n_heads, seq_len, d_head, ct(scale), int(bool(causal)), int(threads))
+    return dq, dk, dv
+
+
+def seeded_inputs(seq_len, n_heads, d_head, seed, std=1.0, with_grad=True):
+    """Q, K, V (and dO) iid N(0, std^2), fp32 [S, H*D], one PCG64 stream per tensor.
+
+    Streams are seeded base+0 (Q), +1 (K), +2 (V), +3 (dO), so a config's
+    inputs are identical wherever they are generated.
+    """
+    dm = n_heads * d_head
+    names = ["q", "k", "v", "do"] if with_grad else ["q", "k", "v"]
+    out = {}
+    for i, name in enumerate(names):
+        rng = np.random.Generator(np.random.PCG64(seed + i))
+        a = rng.standard_normal((seq_len, dm), dtype=np.float32)
+        if std != 1.0:
+            a *= np.float32(std)
+        out[name] = a
+    return out

@@ -1,0 +1,126 @@
+"""The C ABI library on the CPU: it loads, exports every symbol include/*.h declares,
+and rejects bad arguments on the host before any HIP call (so no GPU is needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import dfattn
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "dfattn.h")
+
+
+def declared_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b([A-Za-z_]\w*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "while", "for", "return")))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = dfattn.lib()
+    declared = declared_functions(HEADER)
+    assert "launch_fused_mha_forward" in declared and "dfattn_bwd" in declared
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in dfattn.h but not exported"
+    assert sorted(dfattn.SYMBOLS) == declared
+
+
+def test_reference_symbols_present():
+    # The four launchers and the sync the reference's kernels.rs binds (kernels.rs:9-20, 689-885).
+    for name in ("launch_fused_attention", "launch_fused_mha_forward", "launch_attention_backward",
+                 "launch_fused_mha_backward", "darkforest_sync"):
+        assert name in declared_functions(HEADER)
+
+
+def test_version_and_status_strings():
+    assert "gfx950" in dfattn.version()
+    lib = dfattn.lib()
+    assert lib.dfattn_status_string(0) == b"ok"
+    assert lib.dfattn_status_string(-6) == b"workspace too small"
+    assert lib.dfattn_status_string(-99) == b"unknown status"
+
+
+FAKE = ctypes.c_void_p(0x10000)  # aligned, never dereferenced: validation fails first
+ODD = ctypes.c_void_p(0x10002)   # not 4-byte aligned
+
+
+def fwd(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=None, h=12, s=128, d=64):
+    return dfattn.lib().dfattn_fwd(q, k, v, o, lse, h, s, d, 0.125, 1, None)
+
+
+@pytest.mark.parametrize("kwargs,status", [
+    (dict(q=None), -1), (dict(o=None), -1), (dict(v=ODD), -2), (dict(lse=ODD), -2),
+    (dict(h=0), -3), (dict(s=0), -3), (dict(d=0), -4), (dict(d=129), -4),
+    (dict(h=1 << 21), -5), (dict(s=(1 << 30) + 1), -5),
+])
+def test_forward_validation(kwargs, status):
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    assert fwd(**kwargs) == status
+    assert lib.dfattn_last_error() == status
+    assert lib.dfattn_last_error_message()
+    lib.dfattn_clear_error()
+    assert lib.dfattn_last_error() == 0
+
+
+def bwd(ws=FAKE, ws_bytes=None, h=12, s=1024, d=64, lse=FAKE, o=FAKE):
+    lib = dfattn.lib()
+    if ws_bytes is None:
+        ws_bytes = lib.dfattn_bwd_workspace_bytes(h, s, d)
+    return lib.dfattn_bwd(FAKE, FAKE, FAKE, o, FAKE, lse, FAKE, FAKE, FAKE, ws, ws_bytes, h, s, d, 0.125, 1, None)
+
+
+def test_backward_validation():
+    lib = dfattn.lib()
+    need = lib.dfattn_bwd_workspace_bytes(12, 1024, 64)
+    assert bwd(ws=None) == -6
+    assert bwd(ws_bytes=need - 1) == -6
+    assert bwd(ws=ODD) == -6
+    assert bwd(lse=None) == -1
+    assert bwd(o=None) == -1
+    assert bwd(d=200) == -4
+    assert bwd(s=0) == -3
+    lib.dfattn_clear_error()
+
+
+def test_backward_workspace_is_linear_in_seq_len():
+    lib = dfattn.lib()
+    # Delta [H,S] + per-64-row dO maxima [H, ceil(S/64)] floats, rounded up to 256 bytes.
+    for h, s in ((12, 1024), (12, 4096), (1, 5), (12, 131072)):
+        floats = h * s + h * ((s + 63) // 64)
+        assert lib.dfattn_bwd_workspace_bytes(h, s, 64) == (floats * 4 + 255) // 256 * 256
+    assert lib.dfattn_bwd_workspace_bytes(0, 10, 64) == 0
+    assert lib.dfattn_bwd_workspace_bytes(12, 4096, 64) < 12 * 2 * 4096 * 4096 * 4 // 1000
+
+
+def test_legacy_launcher_records_error_instead_of_launching():
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    # d_head > 128 is a device trap in the reference (attention_fused.cu:56-58); here it is
+    # recorded on the host and reported by darkforest_sync().
+    lib.launch_fused_mha_forward(FAKE, FAKE, FAKE, FAKE, 12, 128, 129, 0.1, 1)
+    assert lib.dfattn_last_error() == -4
+    lib.dfattn_clear_error()
+    lib.launch_fused_mha_backward(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 12, 128, 64, 0.1, 1)
+    assert lib.dfattn_last_error() == -1
+    lib.dfattn_clear_error()
+
+
+def test_product_path_never_touches_the_oracle():
+    """Only tests/, smoke() and bench.py's cpu_baseline may use oracle/."""
+    pkg = os.path.join(ROOT, "dark-forest_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".hpp", ".cpp", ".rs", "Makefile")):
+                text = open(os.path.join(dirpath, f), errors="ignore").read()
+                assert "oracle" not in text.lower(), f"{f} mentions the oracle"
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(dfattn, "_lib", None)
+    monkeypatch.setattr(dfattn, "LIB_PATH", str(tmp_path / "libdfattn.so"))
+    with pytest.raises(dfattn.DfattnNotBuilt):
+        dfattn.lib()
