@@ -66,13 +66,74 @@ def cpu_baseline(heads: int):
             "seconds": round(dt, 3)}
 
 
+TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_c2_hbm_traffic.md")
+KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_main_kernel")
+
+
+def short_kernel_name(name):
+    for k in KERNELS + ("copyBuffer",):
+        if k in name:
+            return k
+    return None
+
+
 def load_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
-        return json.load(f)
+    """HBM bytes per launch of each kernel, from the committed rocprofv3 --pmc summary.
+
+    The summary's table rows read `| kernel | fetch KiB | write KiB | HBM bytes per launch |`.
+    """
+    if not os.path.exists(TRAFFIC_MD):
+        return {}
+    out = {}
+    for line in open(TRAFFIC_MD):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 4 and cells[0] in KERNELS:
+            out[cells[0]] = int(float(cells[3]))
+    return out
+
+
+def summarize_pmc(fetch_csv, write_csv, copy_mib):
+    """Markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE), KiB per dispatch.
+
+    Readings are scaled by what the same counter reads for the plain device copy
+    that `--copy-calibration MIB` runs (MIB MiB read and MIB MiB written).
+    """
+    import csv
+    import collections
+
+    def per_kernel(path, counter):
+        acc = collections.defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            k = short_kernel_name(r["Kernel_Name"])
+            if k and r["Counter_Name"] == counter:
+                acc[k].append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    known_kib = copy_mib * 1024.0
+    f_fac = known_kib / fetch["copyBuffer"]
+    w_fac = known_kib / write["copyBuffer"]
+    lines = [f"Copy calibration ({copy_mib} MiB read + {copy_mib} MiB written): FETCH_SIZE reads "
+             f"{fetch['copyBuffer']:.0f} KiB (factor {f_fac:.3f}), WRITE_SIZE reads {write['copyBuffer']:.0f} KiB "
+             f"(factor {w_fac:.3f}).", "",
+             "| kernel | fetch KiB | write KiB | HBM bytes per launch |", "|---|---|---|---|"]
+    for k in KERNELS:
+        if k in fetch and k in write:
+            total = (fetch[k] * f_fac + write[k] * w_fac) * 1024.0
+            lines.append(f"| {k} | {fetch[k]:.1f} | {write[k]:.1f} | {total:.0f} |")
+    return "\n".join(lines)
+
+
+def summarize_trace(stats_csv):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
+    import csv
+
+    lines = ["| kernel | calls | average us | min us | max us | share |", "|---|---|---|---|---|---|"]
+    for r in csv.DictReader(open(stats_csv)):
+        k = short_kernel_name(r["Name"]) or r["Name"][:40]
+        lines.append(f"| {k} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                     f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |")
+    return "\n".join(lines)
 
 
 def main():
@@ -80,8 +141,21 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-heads", type=int, default=4, help="heads in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-heads", type=int, default=6, help="heads in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after timing, run 5 plain device copies of MIB MiB each (the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM-traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
+                    help="print a rocprofv3 --kernel-trace --stats summary table and exit (no GPU)")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc, args.copy_calibration or 512))
+        return
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -143,8 +217,7 @@ def main():
     traffic = load_traffic()
     roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved, 2), "peak": PEAK_F16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16_TFLOPS, 4),
-                "traffic": (traffic or {}).get(name, {}).get("hbm_bytes_per_launch"),
-                "avg_launch_ms": round(kms, 5)}
+                "traffic": traffic.get(name), "avg_launch_ms": round(kms, 5)}
 
     value = FLOP_STEP / (ms_per_step * 1e-3) / 1e12
     result = {
@@ -173,6 +246,14 @@ def main():
         "roofline": roofline,
         "gpt2_step_ms": None,
     }
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 x {args.copy_calibration} MiB read + {args.copy_calibration} MiB written")
     if args.cpu_heads > 0:
         log(f"cpu baseline on {args.cpu_heads} heads")
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)

@@ -10,17 +10,25 @@
 //  2. bwd_main: a workgroup owns BN = 32*WAVES keys of one head (each wave 32
 //     of them, with its K and V rows held in registers) and streams the query
 //     rows in blocks of BM = 64 through LDS. Per block, on MFMA:
-//        S  = Q K^T, dP = dO V^T                (queries x keys, lane = key)
-//        P  = exp2(S*scale*log2e - lse*log2e)   (recomputed from the forward's lse)
+//        S2 = (c2 Q) K^T, dP = dO V^T           (queries x keys, lane = key)
+//        P  = exp2(S2 - lse*log2e)              (recomputed from the forward's lse)
 //        dS = P * (dP - Delta)
 //        dV += P^T dO, dK += dS^T Q              (keys x d, in registers)
 //        dQ += dS K                              (fp32 atomics into dQ)
 //     dK and dV are written once at the end; no O(S^2) memory is touched.
 //
-// Operands are fp16 (rounded from the fp32 inputs on load), accumulation fp32.
-// dO is multiplied by a per-head power of two sigma before rounding, chosen
-// so max|sigma*dO| lies in [8, 16): training gradients are often far below
-// fp16's normal range. The results are divided by sigma exactly at the end.
+// Numerics. Operands are fp16 (rounded from the fp32 inputs on load),
+// accumulation and softmax fp32. Two rules keep the result within 2e-3
+// max-abs of the fp32 reference without any split-precision products:
+//  * the scores are recomputed with exactly the forward's rounding: Q is
+//    multiplied by c2 = scale*log2(e) before it is rounded, as in
+//    attn_fwd_d64.hip, so P's rows sum to one against the forward's lse;
+//  * Delta is formed from the same fp16-rounded dO that dP is formed from,
+//    so sum_j dS_ij = 0 holds for the rounded operands.
+// The backward is then the exact gradient of attention on fp16-rounded
+// inputs. dO is multiplied by a per-head power of two sigma before rounding,
+// chosen so max|sigma*dO| lies in [8, 16): training gradients are often far
+// below fp16's normal range. The results are divided by sigma exactly.
 #include "dfattn_internal.h"
 
 namespace dfattn {
@@ -32,35 +40,62 @@ constexpr int kPreRows = 64;  // rows per preprocess workgroup
 inline size_t ws_delta_floats(int H, int S) { return (size_t)H * S; }
 inline int pre_blocks(int S) { return (S + kPreRows - 1) / kPreRows; }
 
-// One workgroup = 4 waves handles kPreRows rows of one head (generic in D <= 128).
+// Power of two sigma with max|sigma * x| in [8, 16) for amax = max|x|; 1 if
+// amax is 0 or not finite. Both kernels derive sigma from block maxima with
+// this one function.
+__device__ __forceinline__ float pow2_scale(float amax) {
+  if (!(amax > 0.f) || !(amax < INFINITY)) return 1.f;
+  const int e = max(-126, min(126, 3 - ilogbf(amax)));
+  return ldexpf(1.f, e);
+}
+
+__device__ __forceinline__ float round_f16(float x) { return (float)(half_t)x; }
+
+// One workgroup (256 threads) handles kPreRows = 64 rows of one head, d_head
+// = 64: thread t owns row t/4 and columns 16*(t%4) .. 16*(t%4)+15.
+// Delta of a row is summed from fp16(sigma_b * dO) * O / sigma_b, sigma_b the
+// block's own scale. The main kernel rounds sigma_h * dO with the head's
+// sigma_h <= sigma_b, both powers of two, so both roundings agree wherever
+// sigma_h * dO is an fp16 normal number.
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(
     const float *__restrict__ O, const float *__restrict__ dO, float *__restrict__ dQ,
-    float *__restrict__ delta, float *__restrict__ blockmax, int H, int S, int D) {
+    float *__restrict__ delta, float *__restrict__ blockmax, int H, int S) {
   __shared__ float wmax[4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
-  const size_t ld = (size_t)H * D;
+  const int row = blockIdx.x * kPreRows + (tid >> 2);
+  const bool ok = row < S;
+  const size_t base = ok ? (size_t)row * H * 64 + (size_t)head * 64 + (tid & 3) * 16 : 0;
+  float4 g[4], o[4];
   float mx = 0.f;
-  for (int i = wave; i < kPreRows; i += 4) {
-    const int row = blockIdx.x * kPreRows + i;
-    if (row >= S) break;
-    const size_t base = (size_t)row * ld + (size_t)head * D;
-    float acc = 0.f;
-    for (int d = lane; d < D; d += 64) {
-      const float g = dO[base + d];
-      acc += g * O[base + d];
-      mx = fmaxf(mx, fabsf(g));
-      dQ[base + d] = 0.f;
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) delta[(size_t)head * S + row] = acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    g[i] = load4_or_zero(dO + base + 4 * i, ok);
+    o[i] = load4_or_zero(O + base + 4 * i, ok);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(g[i].x), fabsf(g[i].y)), fmaxf(fabsf(g[i].z), fabsf(g[i].w))));
   }
   mx = wave_max(mx);
   if (lane == 0) wmax[wave] = mx;
   __syncthreads();
-  if (threadIdx.x == 0)
-    blockmax[(size_t)head * gridDim.x + blockIdx.x] =
-        fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float bmax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float sig = pow2_scale(bmax);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc += round_f16(g[i].x * sig) * o[i].x;
+    acc += round_f16(g[i].y * sig) * o[i].y;
+    acc += round_f16(g[i].z * sig) * o[i].z;
+    acc += round_f16(g[i].w * sig) * o[i].w;
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  if (ok) {
+    if ((tid & 3) == 0) delta[(size_t)head * S + row] = acc / sig;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<float4 *>(dQ + base + 4 * i) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tid == 0) blockmax[(size_t)head * gridDim.x + blockIdx.x] = bmax;
 }
 
 template <int WAVES>
@@ -118,7 +153,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
   for (int i = lane; i < n_pre_blocks; i += 64)
     gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
   gmax = wave_max(gmax);
-  const float sigma = (gmax > 0.f && gmax < INFINITY) ? ldexpf(1.f, 3 - ilogbf(gmax)) : 1.f;
+  const float sigma = pow2_scale(gmax);
   const float inv_sigma = 1.f / sigma;
   const float c2 = scale * kLog2e;
 
@@ -174,6 +209,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
     for (int i = 0; i < C::PAIRS; ++i) {
       const int idx = tid + i * C::THREADS;
       const int rp = idx >> 4, c4 = idx & 15;
+      qreg[2 * i] = scale4(qreg[2 * i], c2);
+      qreg[2 * i + 1] = scale4(qreg[2 * i + 1], c2);
       const float4 d0 = scale4(doreg[2 * i], sigma), d1 = scale4(doreg[2 * i + 1], sigma);
       *reinterpret_cast<half4_t *>(q_lds + (2 * rp) * C::QS + c4 * 4) = to_half4(qreg[2 * i]);
       *reinterpret_cast<half4_t *>(q_lds + (2 * rp + 1) * C::QS + c4 * 4) = to_half4(qreg[2 * i + 1]);
@@ -238,7 +275,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          float p = fast_exp2(sacc[qb][r] * c2 - f4at(L, e));
+          float p = fast_exp2(sacc[qb][r] - f4at(L, e));
           if (causal && key > qb0 + ql + e) p = 0.f;
           sacc[qb][r] = p;
           pacc[qb][r] = p * (pacc[qb][r] - f4at(Dl, e));
@@ -307,9 +344,9 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
     }
   }
 
-  // dK = scale * dS^T Q / sigma, dV = P^T dO / sigma; row r is key
-  // kv_blk0 + 32*wave + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
-  const float dk_scale = scale * inv_sigma;
+  // dK = scale * dS^T Q = ln2 * dS^T (c2 Q) / sigma, dV = P^T dO / sigma; row
+  // r is key kv_blk0 + 32*wave + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
+  const float dk_scale = kLn2 * inv_sigma;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int kr = kv_blk0 + wave * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
@@ -337,7 +374,7 @@ hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, float *d_q, void
   float *delta = static_cast<float *>(workspace);
   float *blockmax = delta + ws_delta_floats(n_heads, seq_len);
   hipLaunchKernelGGL(bwd_preprocess_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream,
-                     o, d_o, d_q, delta, blockmax, n_heads, seq_len, 64);
+                     o, d_o, d_q, delta, blockmax, n_heads, seq_len);
   return hipGetLastError();
 }
 
