@@ -180,7 +180,7 @@ def main():
         dfattn.attention_forward(q, k, v, H, SCALE, True, out=o, lse=lse)
         if ev is not None:
             ev[1].record(stream)
-        dfattn.backward_preprocess(o, g, dq, ws, H)
+        dfattn.backward_preprocess(o, g, ws, H)
         if ev is not None:
             ev[2].record(stream)
         dfattn.backward_main(q, k, v, g, lse, dq, dk, dv, ws, H, SCALE, True)

@@ -3,32 +3,31 @@
 // Replaces kernel_mha_bwd_all_heads (darkforest-cuda/kernels/attention_fused.cu:390-516),
 // which recomputes each row's softmax with four serial passes over the keys,
 // stores P and dS in an [H, 2, S, S] fp32 scratch and accumulates dK and dV
-// with one atomicAdd per (query, key, d). Here:
+// with one atomicAdd per (query, key, d). Here, with no O(S^2) memory and no
+// atomics:
 //
-//  1. bwd_preprocess: Delta_i = dO_i . O_i per (head, row), the per-block
-//     max |dO| (for a power-of-two operand scale of dO, see below), and dQ := 0.
-//  2. bwd_main: a workgroup owns BN = 32*WAVES keys of one head (each wave 32
-//     of them, with its K and V rows held in registers) and streams the query
-//     rows in blocks of BM = 64 through LDS. Per block, on MFMA:
-//        S2 = (c2 Q) K^T, dP = dO V^T           (queries x keys, lane = key)
-//        P  = exp2(S2 - lse*log2e)              (recomputed from the forward's lse)
-//        dS = P * (dP - Delta)
-//        dV += P^T dO, dK += dS^T Q              (keys x d, in registers)
-//        dQ += dS K                              (fp32 atomics into dQ)
-//     dK and dV are written once at the end; no O(S^2) memory is touched.
+//  1. bwd_preprocess: Delta_i = dO_i . O_i per (head, row) and the per-block
+//     max |dO| (for a power-of-two operand scale of dO, see below).
+//  2. bwd_main, one launch holding two kinds of workgroup, interleaved
+//     longest-first so both fill the chip together:
+//     * dK/dV workgroups own 128 keys of one head (32 per wave, their K and V
+//       rows held in registers) and stream the query rows in blocks of 64
+//       through LDS:
+//          S = (c2 Q) K^T, dP = dO V^T         (queries x keys, lane = key)
+//          P = exp2(S - lse*log2e), dS = P * (dP - Delta)
+//          dV += P^T dO, dK += dS^T (c2 Q)      (keys x d, in registers)
+//     * dQ workgroups own 128 query rows (32 per wave, Q and dO in
+//       registers) and stream the keys in tiles of 64 through LDS:
+//          S^T = K (c2 Q)^T, dP^T = V dO^T      (keys x queries, lane = query)
+//          dQ^T += K^T dS^T                     (d x queries, in registers)
+//     Recomputing S and dP for dQ costs two more products than accumulating
+//     dQ with atomics from the dK/dV workgroups, and removes the atomics'
+//     traffic (one fp32 read-modify-write per query, column and key block).
 //
-// Numerics. Operands are fp16 (rounded from the fp32 inputs on load),
-// accumulation and softmax fp32. Two rules keep the result within 2e-3
-// max-abs of the fp32 reference without any split-precision products:
-//  * the scores are recomputed with exactly the forward's rounding: Q is
-//    multiplied by c2 = scale*log2(e) before it is rounded, as in
-//    attn_fwd_d64.hip, so P's rows sum to one against the forward's lse;
-//  * Delta is formed from the same fp16-rounded dO that dP is formed from,
-//    so sum_j dS_ij = 0 holds for the rounded operands.
-// The backward is then the exact gradient of attention on fp16-rounded
-// inputs. dO is multiplied by a per-head power of two sigma before rounding,
-// chosen so max|sigma*dO| lies in [8, 16): training gradients are often far
-// below fp16's normal range. The results are divided by sigma exactly.
+// Operands that must be transposed (dO^T and Q^T for dV and dK, K^T for dQ)
+// come from the same row-major swizzled tiles through the transposing LDS
+// read, with k-slots in the row order of the P and dS registers they pair with.
+//
 #include "dfattn_internal.h"
 
 namespace dfattn {
@@ -58,8 +57,8 @@ __device__ __forceinline__ float round_f16(float x) { return (float)(half_t)x; }
 // sigma_h <= sigma_b, both powers of two, so both roundings agree wherever
 // sigma_h * dO is an fp16 normal number.
 __global__ __launch_bounds__(256) void bwd_preprocess_kernel(
-    const float *__restrict__ O, const float *__restrict__ dO, float *__restrict__ dQ,
-    float *__restrict__ delta, float *__restrict__ blockmax, int H, int S) {
+    const float *__restrict__ O, const float *__restrict__ dO, float *__restrict__ delta,
+    float *__restrict__ blockmax, int H, int S) {
   __shared__ float wmax[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
@@ -89,85 +88,84 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
-  if (ok) {
-    if ((tid & 3) == 0) delta[(size_t)head * S + row] = acc / sig;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<float4 *>(dQ + base + 4 * i) = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  if (ok && (tid & 3) == 0) delta[(size_t)head * S + row] = acc / sig;
   if (tid == 0) blockmax[(size_t)head * gridDim.x + blockIdx.x] = bmax;
 }
 
-template <int WAVES>
-struct BwdCfg {
-  static constexpr int D = 64;
-  static constexpr int BN = 32 * WAVES;  // keys per workgroup
-  static constexpr int BM = 64;          // query rows per iteration
-  static constexpr int THREADS = 64 * WAVES;
-  static constexpr int QS = D + 8;       // [BM][QS] row-major Q and dO
-  static constexpr int TS = BM + 8;      // [D][TS] transposed Q^T and dO^T
-  static constexpr int DSS = BN + 8;     // [BM][DSS] dS
-  static constexpr int KTS = BN + 8;     // [D][KTS] K^T
-  static constexpr int PAIRS = (BM / 2) * (D / 4) / THREADS;  // staging items per thread
-  static_assert(PAIRS * THREADS * 8 == BM * D, "staging split");
-  static constexpr int OFF_Q = 0;
-  static constexpr int OFF_QT = OFF_Q + BM * QS;
-  static constexpr int OFF_DO = OFF_QT + D * TS;
-  static constexpr int OFF_DOT = OFF_DO + BM * QS;
-  static constexpr int OFF_DS = OFF_DOT + D * TS;
-  static constexpr int OFF_KT = OFF_DS + BM * DSS;
-  static constexpr int HALVES = OFF_KT + D * KTS;
-  static constexpr int DQ_TILES = 4 / WAVES > 0 ? 4 / WAVES : 1;  // 32x32 dQ tiles per wave
-  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "waves");
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kD = 64;
+constexpr int kKeysPerWg = 128;     // dK/dV workgroup: keys owned (4 groups of 32)
+constexpr int kQBlock = 64;         // dK/dV workgroup: query rows per step (2 halves of 32)
+constexpr int kQueriesPerWg = 128;  // dQ workgroup: query rows owned (4 groups of 32)
+constexpr int kKTile = 64;          // dQ workgroup: keys per step (2 halves of 32)
+constexpr int kTile = 64 * kD;      // halves per staged [64][64] tile
+constexpr int kStageF4 = 64 * kD / 4 / kThreads;  // float4 per thread per staged tile
+static_assert(kStageF4 * kThreads * 4 == 64 * kD, "staging split");
+// LDS: two stages of two tiles; after the loop the same bytes carry the
+// partner waves' partial results (4 waves x 32 registers x 64 lanes fp32).
+constexpr int kLdsBytes = 2 * 2 * kTile * 2 > 4 * 32 * 64 * 4 ? 2 * 2 * kTile * 2 : 4 * 32 * 64 * 4;
+
+struct BwdArgs {
+  const float *Q, *K, *V, *dO, *LSE, *delta, *blockmax;
+  float *dQ, *dK, *dV;
+  int H, S, causal, n_pre_blocks;
+  float scale;
 };
 
-__device__ __forceinline__ float f4at(const float4 &v, int e) {
-  return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+// Per-head sigma (power of two) from the preprocess block maxima of |dO|.
+__device__ __forceinline__ float head_sigma(const BwdArgs &a, int head, int lane) {
+  float gmax = 0.f;
+  for (int i = lane; i < a.n_pre_blocks; i += 64)
+    gmax = fmaxf(gmax, a.blockmax[(size_t)head * a.n_pre_blocks + i]);
+  return pow2_scale(wave_max(gmax));
 }
 
-template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
-    const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
-    const float *__restrict__ dO, const float *__restrict__ LSE,
-    const float *__restrict__ delta, const float *__restrict__ blockmax,
-    float *__restrict__ dQ, float *__restrict__ dK, float *__restrict__ dV, int H, int S,
-    float scale, int causal, int n_pre_blocks) {
-  using C = BwdCfg<WAVES>;
-  __shared__ __attribute__((aligned(16))) half_t lds[C::HALVES];
-  __shared__ __attribute__((aligned(16))) float lse2_lds[C::BM];
-  __shared__ __attribute__((aligned(16))) float delta_lds[C::BM];
+// Partner waves (w, w+4) hold partial sums of the same 32x32 accumulator
+// blocks: wave w+4 hands its two blocks to wave w through LDS (after a
+// barrier that ends all use of the staging tiles), wave w adds them.
+__device__ __forceinline__ void merge_pair(float *buf, int wave, int lane, f32x16 &x0, f32x16 &x1) {
+  float *mine = buf + (size_t)(wave & 3) * 32 * 64;
+  if (wave >= 4) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      mine[r * 64 + lane] = x0[r];
+      mine[(16 + r) * 64 + lane] = x1[r];
+    }
+  }
+  __syncthreads();
+  if (wave < 4) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x0[r] += mine[r * 64 + lane];
+      x1[r] += mine[(16 + r) * 64 + lane];
+    }
+  }
+  __syncthreads();
+}
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+// dK and dV of keys [kv_blk0, kv_blk0 + 128) of one head. Wave w owns keys
+// kv_blk0 + 32*(w%4) .. +31 and query half w/4 of every 64-row block.
+__device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char *lds_raw,
+                          float (*stat)[2][kQBlock]) {
+  half_t(*lds)[2][kTile] = reinterpret_cast<half_t(*)[2][kTile]>(lds_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, hh = lane >> 5;
-  const int head = blockIdx.x % H;
-  const int kvtile = blockIdx.x / H;  // tile 0 sees the most queries: launched first
-  const size_t ld = (size_t)H * C::D;
-  const size_t hoff = (size_t)head * C::D;
-  const int kv_blk0 = kvtile * C::BN;
-  const int key = kv_blk0 + wave * 32 + c;  // this lane's key (B/A operand column)
+  const int kg = wave & 3, qh = wave >> 2;
+  const int S = a.S;
+  const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
+  const float sigma = head_sigma(a, head, lane);
+  const float c2 = a.scale * kLog2e;
+  const int key0 = kv_blk0 + kg * 32;  // this wave's first key
+  const int key = key0 + c;
   const bool key_ok = key < S;
 
-  // Per-head power-of-two scale of dO.
-  float gmax = 0.f;
-  for (int i = lane; i < n_pre_blocks; i += 64)
-    gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
-  gmax = wave_max(gmax);
-  const float sigma = pow2_scale(gmax);
-  const float inv_sigma = 1.f / sigma;
-  const float c2 = scale * kLog2e;
-
-  half_t *q_lds = lds + C::OFF_Q, *qt_lds = lds + C::OFF_QT;
-  half_t *do_lds = lds + C::OFF_DO, *dot_lds = lds + C::OFF_DOT;
-  half_t *ds_lds = lds + C::OFF_DS, *kt_lds = lds + C::OFF_KT;
-
   // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
-  // holds this lane's key, slots d = 16*ds + 8*hh + j. K^T also goes to LDS
-  // for the dQ product.
+  // holds its key, slots d = 16*ds + 8*hh + j.
   half8_t kf[4], vf[4];
   {
-    const float *kp = K + (key_ok ? (size_t)key * ld + hoff : 0);
-    const float *vp = V + (key_ok ? (size_t)key * ld + hoff : 0);
+    const float *kp = a.K + (key_ok ? (size_t)key * ld + hoff : 0);
+    const float *vp = a.V + (key_ok ? (size_t)key * ld + hoff : 0);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
       const half4_t k0 = to_half4(load4_or_zero(kp + ds * 16 + hh * 8, key_ok));
@@ -176,189 +174,289 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_main_kernel(
       const half4_t v1 = to_half4(load4_or_zero(vp + ds * 16 + hh * 8 + 4, key_ok));
       kf[ds] = half8_t{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
       vf[ds] = half8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kt_lds[(ds * 16 + hh * 8 + j) * C::KTS + wave * 32 + c] = kf[ds][j];
     }
   }
 
-  // Staging registers for one query block (prefetched one iteration ahead).
-  float4 qreg[2 * C::PAIRS], doreg[2 * C::PAIRS];
+  float4 qreg[kStageF4], doreg[kStageF4];
   float lreg = 0.f, dreg = 0.f;
-  auto load_stage = [&](int qb0) {
+  auto load_block = [&](int qb0) {
 #pragma unroll
-    for (int i = 0; i < C::PAIRS; ++i) {
-      const int idx = tid + i * C::THREADS;
-      const int row = qb0 + 2 * (idx >> 4), c4 = idx & 15;
-      const bool ok0 = row < S, ok1 = row + 1 < S;
-      const size_t o0 = ok0 ? (size_t)row * ld + hoff + c4 * 4 : 0;
-      const size_t o1 = ok1 ? (size_t)(row + 1) * ld + hoff + c4 * 4 : 0;
-      qreg[2 * i] = load4_or_zero(Q + o0, ok0);
-      qreg[2 * i + 1] = load4_or_zero(Q + o1, ok1);
-      doreg[2 * i] = load4_or_zero(dO + o0, ok0);
-      doreg[2 * i + 1] = load4_or_zero(dO + o1, ok1);
+    for (int i = 0; i < kStageF4; ++i) {
+      // Rows past the end read row S-1 (finite); their lse is +inf, so P = 0.
+      const int idx = tid + i * kThreads;
+      const int row = min(qb0 + (idx >> 4), S - 1), c4 = idx & 15;
+      const size_t off = (size_t)row * ld + hoff + c4 * 4;
+      qreg[i] = *reinterpret_cast<const float4 *>(a.Q + off);
+      doreg[i] = *reinterpret_cast<const float4 *>(a.dO + off);
     }
-    if (tid < C::BM) {
+    if (tid < kQBlock) {
       const int row = qb0 + tid;
       const bool ok = row < S;
-      lreg = ok ? LSE[(size_t)head * S + row] * kLog2e : INFINITY;
-      dreg = ok ? delta[(size_t)head * S + row] : 0.f;
+      lreg = ok ? a.LSE[(size_t)head * S + row] * kLog2e : INFINITY;
+      dreg = ok ? a.delta[(size_t)head * S + row] : 0.f;
     }
   };
-  auto store_stage = [&]() {
+  auto store_block = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < C::PAIRS; ++i) {
-      const int idx = tid + i * C::THREADS;
-      const int rp = idx >> 4, c4 = idx & 15;
-      qreg[2 * i] = scale4(qreg[2 * i], c2);
-      qreg[2 * i + 1] = scale4(qreg[2 * i + 1], c2);
-      const float4 d0 = scale4(doreg[2 * i], sigma), d1 = scale4(doreg[2 * i + 1], sigma);
-      *reinterpret_cast<half4_t *>(q_lds + (2 * rp) * C::QS + c4 * 4) = to_half4(qreg[2 * i]);
-      *reinterpret_cast<half4_t *>(q_lds + (2 * rp + 1) * C::QS + c4 * 4) = to_half4(qreg[2 * i + 1]);
-      *reinterpret_cast<half4_t *>(do_lds + (2 * rp) * C::QS + c4 * 4) = to_half4(d0);
-      *reinterpret_cast<half4_t *>(do_lds + (2 * rp + 1) * C::QS + c4 * 4) = to_half4(d1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        half2_t pq, pd;
-        pq[0] = (half_t)f4at(qreg[2 * i], e);
-        pq[1] = (half_t)f4at(qreg[2 * i + 1], e);
-        pd[0] = (half_t)f4at(d0, e);
-        pd[1] = (half_t)f4at(d1, e);
-        *reinterpret_cast<half2_t *>(qt_lds + (c4 * 4 + e) * C::TS + 2 * rp) = pq;
-        *reinterpret_cast<half2_t *>(dot_lds + (c4 * 4 + e) * C::TS + 2 * rp) = pd;
-      }
+    for (int i = 0; i < kStageF4; ++i) {
+      const int idx = tid + i * kThreads;
+      tile_store4(lds[st][0], idx >> 4, (idx & 15) * 4, scale4(qreg[i], c2));
+      tile_store4(lds[st][1], idx >> 4, (idx & 15) * 4, scale4(doreg[i], sigma));
     }
-    if (tid < C::BM) {
-      lse2_lds[tid] = lreg;
-      delta_lds[tid] = dreg * sigma;
+    if (tid < kQBlock) {  // negated: they enter the products as accumulator inputs
+      stat[st][0][tid] = -lreg;
+      stat[st][1][tid] = -(dreg * sigma);
     }
   };
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
 
-  const int n_qblocks = (S + C::BM - 1) / C::BM;
-  const int first_qb = causal ? kv_blk0 / C::BM : 0;
-  if (first_qb < n_qblocks) load_stage(first_qb * C::BM);
+  const int n_qblocks = (S + kQBlock - 1) / kQBlock;
+  const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
+  if (first_qb < n_qblocks) {
+    load_block(first_qb * kQBlock);
+    store_block(0);
+  }
+  __syncthreads();
 
   for (int qbi = first_qb; qbi < n_qblocks; ++qbi) {
-    const int qb0 = qbi * C::BM;
-    __syncthreads();  // previous block's LDS reads are done
-    store_stage();
-    __syncthreads();  // staged block visible
-    if (qbi + 1 < n_qblocks) load_stage(qb0 + C::BM);
+    const int st = (qbi - first_qb) & 1;
+    const int qb0 = qbi * kQBlock;
+    const int q0 = qb0 + qh * 32;  // this wave's first query row
+    if (qbi + 1 < n_qblocks) load_block(qb0 + kQBlock);
+    // Rows q0..q0+31 see this wave's keys only if some row >= key0.
+    if (!a.causal || q0 + 31 >= key0) {
+      const half_t *qt = lds[st][0];
+      const half_t *dot = lds[st][1];
 
-    // S and dP for the two 32-row halves of the block (rows = queries, lane = key).
-    f32x16 sacc[2], pacc[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      sacc[qb] = f32x16{};
-      pacc[qb] = f32x16{};
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const half8_t aq =
-            *reinterpret_cast<const half8_t *>(q_lds + (qb * 32 + c) * C::QS + ds * 16 + hh * 8);
-        const half8_t ad =
-            *reinterpret_cast<const half8_t *>(do_lds + (qb * 32 + c) * C::QS + ds * 16 + hh * 8);
-        sacc[qb] = mfma32x32x16(aq, kf[ds], sacc[qb]);
-        pacc[qb] = mfma32x32x16(ad, vf[ds], pacc[qb]);
-      }
-    }
-
-    // P and dS; register r of half qb is query qb0 + 32*qb + 8*(r/4) + 4*hh + r%4.
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+      // S - lse2 and dP - Delta: register r is query q0 + 8*(r/4) + 4*hh + r%4
+      // (lane = key); the first MFMA of each chain takes the row's -lse2 /
+      // -Delta as its accumulator input.
+      f32x16 s, dp;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int ql = qb * 32 + g * 8 + hh * 4;
-        const float4 L = *reinterpret_cast<const float4 *>(lse2_lds + ql);
-        const float4 Dl = *reinterpret_cast<const float4 *>(delta_lds + ql);
+        const float4 nl = *reinterpret_cast<const float4 *>(&stat[st][0][qh * 32 + g * 8 + hh * 4]);
+        const float4 nd = *reinterpret_cast<const float4 *>(&stat[st][1][qh * 32 + g * 8 + hh * 4]);
+        s[4 * g] = nl.x; s[4 * g + 1] = nl.y; s[4 * g + 2] = nl.z; s[4 * g + 3] = nl.w;
+        dp[4 * g] = nd.x; dp[4 * g + 1] = nd.y; dp[4 * g + 2] = nd.z; dp[4 * g + 3] = nd.w;
+      }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g + e;
-          float p = fast_exp2(sacc[qb][r] - f4at(L, e));
-          if (causal && key > qb0 + ql + e) p = 0.f;
-          sacc[qb][r] = p;
-          pacc[qb][r] = p * (pacc[qb][r] - f4at(Dl, e));
-        }
+      for (int ds = 0; ds < 4; ++ds) {
+        s = mfma32x32x16(tile_row8(qt, qh * 32 + c, 2 * ds + hh), kf[ds], s);
+        dp = mfma32x32x16(tile_row8(dot, qh * 32 + c, 2 * ds + hh), vf[ds], dp);
       }
 
-    // P^T and dS^T as A operands (M = keys): query step qs covers queries
-    // 16*qs + (8*(j/4) + 4*hh + j%4) in slot j.
-    half8_t pf[4], dsf[4];
+      // P and dS (dS overwrites dP).
+      if (a.causal && q0 < key0 + 31) {
 #pragma unroll
-    for (int qs = 0; qs < 4; ++qs) {
-      const int base = (qs & 1) * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pf[qs][j] = (half_t)sacc[qs >> 1][base + j];
-        dsf[qs][j] = (half_t)pacc[qs >> 1][base + j];
+        for (int r = 0; r < 16; ++r)
+          if (key > q0 + (r >> 2) * 8 + hh * 4 + (r & 3)) s[r] = -INFINITY;
       }
-    }
-
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int qs = 0; qs < 4; ++qs) {
-        const int off = (db * 32 + c) * C::TS + qs * 16 + hh * 4;
-        const half4_t d0 = *reinterpret_cast<const half4_t *>(dot_lds + off);
-        const half4_t d1 = *reinterpret_cast<const half4_t *>(dot_lds + off + 8);
-        const half4_t q0 = *reinterpret_cast<const half4_t *>(qt_lds + off);
-        const half4_t q1 = *reinterpret_cast<const half4_t *>(qt_lds + off + 8);
-        const half8_t bdo = half8_t{d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
-        const half8_t bq = half8_t{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
-        dv[db] = mfma32x32x16(pf[qs], bdo, dv[db]);
-        dk[db] = mfma32x32x16(dsf[qs], bq, dk[db]);
-      }
-
-    // dS -> LDS, query-major, for dQ = dS K.
-#pragma unroll
-    for (int qs = 0; qs < 4; ++qs)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int ql = qs * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
-        ds_lds[ql * C::DSS + wave * 32 + c] = dsf[qs][j];
-      }
-    __syncthreads();
-
-    // dQ block (64 x 64) = dS (64 x BN) . K (BN x 64), split in 32x32 tiles.
-#pragma unroll
-    for (int tt = 0; tt < C::DQ_TILES; ++tt) {
-      const int tile = wave * C::DQ_TILES + tt;
-      const int qt = tile >> 1, dt = tile & 1;
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < C::BN / 16; ++ks) {
-        const half8_t a =
-            *reinterpret_cast<const half8_t *>(ds_lds + (qt * 32 + c) * C::DSS + ks * 16 + hh * 8);
-        const half8_t b =
-            *reinterpret_cast<const half8_t *>(kt_lds + (dt * 32 + c) * C::KTS + ks * 16 + hh * 8);
-        acc = mfma32x32x16(a, b, acc);
-      }
-      const float dq_scale = scale * inv_sigma;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int query = qb0 + qt * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-        if (query < S)
-          unsafeAtomicAdd(dQ + (size_t)query * ld + hoff + dt * 32 + c, acc[r] * dq_scale);
+        s[r] = fast_exp2(s[r]);
+        dp[r] *= s[r];
+      }
+
+      // dV += P^T dO, dK += dS^T (c2 Q): A from registers (lane = key), B =
+      // dO^T / Q^T through transposed reads of this wave's 32 rows.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8_t pf = acc_to_slots(s, j);
+        const half8_t dsf = acc_to_slots(dp, j);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          dv[db] = mfma32x32x16(pf, tile_tr8(dot, 2 * qh + j, db, lane), dv[db]);
+          dk[db] = mfma32x32x16(dsf, tile_tr8(qt, 2 * qh + j, db, lane), dk[db]);
+        }
       }
     }
+    if (qbi + 1 < n_qblocks) store_block(st ^ 1);
+    __syncthreads();
   }
 
+  float *buf = reinterpret_cast<float *>(lds_raw);
+  merge_pair(buf, wave, lane, dk[0], dk[1]);
+  merge_pair(buf, wave, lane, dv[0], dv[1]);
+  if (wave >= 4) return;
+
   // dK = scale * dS^T Q = ln2 * dS^T (c2 Q) / sigma, dV = P^T dO / sigma; row
-  // r is key kv_blk0 + 32*wave + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
-  const float dk_scale = kLn2 * inv_sigma;
+  // r is key key0 + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
+  const float dk_scale = kLn2 / sigma, dv_scale = 1.f / sigma;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int kr = kv_blk0 + wave * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+    const int kr = key0 + (r >> 2) * 8 + hh * 4 + (r & 3);
     if (kr < S) {
-      float *dkrow = dK + (size_t)kr * ld + hoff;
-      float *dvrow = dV + (size_t)kr * ld + hoff;
+      float *dkrow = a.dK + (size_t)kr * ld + hoff;
+      float *dvrow = a.dV + (size_t)kr * ld + hoff;
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
         dkrow[db * 32 + c] = dk[db][r] * dk_scale;
-        dvrow[db * 32 + c] = dv[db][r] * inv_sigma;
+        dvrow[db * 32 + c] = dv[db][r] * dv_scale;
       }
     }
+  }
+}
+
+// dQ of query rows [q_blk0, q_blk0 + 128) of one head. Wave w owns rows
+// q_blk0 + 32*(w%4) .. +31 and key half w/4 of every 64-key tile.
+__device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *lds_raw) {
+  half_t(*lds)[2][kTile] = reinterpret_cast<half_t(*)[2][kTile]>(lds_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, hh = lane >> 5;
+  const int qg = wave & 3, kh = wave >> 2;
+  const int S = a.S;
+  const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
+  const float sigma = head_sigma(a, head, lane);
+  const float c2 = a.scale * kLog2e;
+  const int q_w0 = q_blk0 + qg * 32;
+  const int query = q_w0 + c;
+  const bool q_ok = query < S;
+  const bool wave_active = q_w0 < S;
+  const int wave_qlast = min(q_w0 + 32, S) - 1;
+  // Keys above key_lim are masked for this lane's row; no key of a half tile
+  // starting at k0 is masked for any row of the wave when k0 + 31 <= key_lim_lo.
+  const int key_lim = a.causal ? min(query, S - 1) : S - 1;
+  const int key_lim_lo = a.causal ? min(q_w0, S - 1) : S - 1;
+
+  // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds its query.
+  half8_t qf[4], gf[4];
+  {
+    const float *qp = a.Q + (q_ok ? (size_t)query * ld + hoff : 0);
+    const float *gp = a.dO + (q_ok ? (size_t)query * ld + hoff : 0);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const half4_t q0 = to_half4(scale4(load4_or_zero(qp + ds * 16 + hh * 8, q_ok), c2));
+      const half4_t q1 = to_half4(scale4(load4_or_zero(qp + ds * 16 + hh * 8 + 4, q_ok), c2));
+      const half4_t g0 = to_half4(scale4(load4_or_zero(gp + ds * 16 + hh * 8, q_ok), sigma));
+      const half4_t g1 = to_half4(scale4(load4_or_zero(gp + ds * 16 + hh * 8 + 4, q_ok), sigma));
+      qf[ds] = half8_t{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+      gf[ds] = half8_t{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    }
+  }
+  const float L = q_ok ? a.LSE[(size_t)head * S + query] * kLog2e : INFINITY;
+  const float Dl = q_ok ? a.delta[(size_t)head * S + query] * sigma : 0.f;
+  f32x16 negL, negD;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    negL[r] = -L;
+    negD[r] = -Dl;
+  }
+
+  const int kv_end = a.causal ? min(S, q_blk0 + kQueriesPerWg) : S;
+  const int n_tiles = (kv_end + kKTile - 1) / kKTile;
+
+  float4 kreg[kStageF4], vreg[kStageF4];
+  auto load_tile = [&](int t) {
+    const int kv0 = t * kKTile;
+#pragma unroll
+    for (int i = 0; i < kStageF4; ++i) {
+      // Keys past the end read row S-1 (finite) and are masked to P = 0.
+      const int idx = tid + i * kThreads;
+      const int kr = min(kv0 + (idx >> 4), S - 1), c4 = idx & 15;
+      const size_t off = (size_t)kr * ld + hoff + c4 * 4;
+      kreg[i] = *reinterpret_cast<const float4 *>(a.K + off);
+      vreg[i] = *reinterpret_cast<const float4 *>(a.V + off);
+    }
+  };
+  auto store_tile = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < kStageF4; ++i) {
+      const int idx = tid + i * kThreads;
+      tile_store4(lds[st][0], idx >> 4, (idx & 15) * 4, kreg[i]);
+      tile_store4(lds[st][1], idx >> 4, (idx & 15) * 4, vreg[i]);
+    }
+  };
+
+  f32x16 dq[2];
+  dq[0] = dq[1] = f32x16{};
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int st = t & 1;
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    const int k0 = t * kKTile + kh * 32;  // first key of this wave's half tile
+    if (wave_active && k0 < S && (!a.causal || k0 <= wave_qlast)) {
+      const half_t *kt = lds[st][0];
+      const half_t *vt = lds[st][1];
+      // S^T - lse2 and dP^T - Delta: register r is key k0 + 8*(r/4) + 4*hh +
+      // r%4 (lane = query); the chains start from the lane's -lse2 / -Delta.
+      f32x16 s = mfma32x32x16(tile_row8(kt, kh * 32 + c, hh), qf[0], negL);
+      f32x16 dp = mfma32x32x16(tile_row8(vt, kh * 32 + c, hh), gf[0], negD);
+#pragma unroll
+      for (int ds = 1; ds < 4; ++ds) {
+        s = mfma32x32x16(tile_row8(kt, kh * 32 + c, 2 * ds + hh), qf[ds], s);
+        dp = mfma32x32x16(tile_row8(vt, kh * 32 + c, 2 * ds + hh), gf[ds], dp);
+      }
+      if (k0 + 31 > key_lim_lo) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] *= fast_exp2(s[r]);
+      // dQ^T += K^T dS^T over this wave's two key steps; K^T through
+      // transposed reads of the K tile.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8_t dsf = acc_to_slots(dp, j);
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+          dq[db] = mfma32x32x16(tile_tr8(kt, 2 * kh + j, db, lane), dsf, dq[db]);
+      }
+    }
+    if (t + 1 < n_tiles) store_tile(st ^ 1);
+    __syncthreads();
+  }
+
+  merge_pair(reinterpret_cast<float *>(lds_raw), wave, lane, dq[0], dq[1]);
+  if (wave >= 4) return;
+
+  // dQ = scale * dS K / sigma; register r of block db is column 32*db + 8*(r/4) + 4*hh + r%4.
+  if (q_ok) {
+    const float dq_scale = a.scale / sigma;
+    float *qrow = a.dQ + (size_t)query * ld + hoff;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4 *>(qrow + db * 32 + g * 8 + hh * 4) =
+            make_float4(dq[db][4 * g] * dq_scale, dq[db][4 * g + 1] * dq_scale,
+                        dq[db][4 * g + 2] * dq_scale, dq[db][4 * g + 3] * dq_scale);
+  }
+}
+
+// Workgroup b: the two item lists (dK/dV key tiles, dQ query tiles), each
+// ordered longest first under causal masking and round robin over heads,
+// alternate while both last; the longer list's remainder follows.
+__global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, int n_kv_items,
+                                                             int n_q_items) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) float stat[2][2][kQBlock];
+  const int b = blockIdx.x;
+  const int pairs = min(n_kv_items, n_q_items);
+  bool kv_item;
+  int item;
+  if (b < 2 * pairs) {
+    kv_item = (b & 1) == 0;
+    item = b >> 1;
+  } else {
+    kv_item = n_kv_items > n_q_items;
+    item = b - pairs;
+  }
+  const int head = item % a.H;
+  const int rank = item / a.H;
+  if (kv_item) {
+    dkdv_path(a, head, rank * kKeysPerWg, lds_raw, stat);  // key tile 0 sees the most queries
+  } else {
+    const int n_qtiles = n_q_items / a.H;
+    const int qtile = a.causal ? n_qtiles - 1 - rank : rank;
+    dq_path(a, head, qtile * kQueriesPerWg, lds_raw);
   }
 }
 
@@ -369,12 +467,12 @@ size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) {
   return (floats * sizeof(float) + 255) / 256 * 256;
 }
 
-hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, float *d_q, void *workspace,
-                              int n_heads, int seq_len, hipStream_t stream) {
+hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, void *workspace, int n_heads,
+                              int seq_len, hipStream_t stream) {
   float *delta = static_cast<float *>(workspace);
   float *blockmax = delta + ws_delta_floats(n_heads, seq_len);
   hipLaunchKernelGGL(bwd_preprocess_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream,
-                     o, d_o, d_q, delta, blockmax, n_heads, seq_len);
+                     o, d_o, delta, blockmax, n_heads, seq_len);
   return hipGetLastError();
 }
 
@@ -382,14 +480,26 @@ hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, c
                                const float *lse, float *d_q, float *d_k, float *d_v,
                                const void *workspace, int n_heads, int seq_len, float scale,
                                bool causal, hipStream_t stream) {
-  constexpr int WAVES = 4;
-  using C = BwdCfg<WAVES>;
-  const float *delta = static_cast<const float *>(workspace);
-  const float *blockmax = delta + ws_delta_floats(n_heads, seq_len);
-  const int n_kvtiles = (seq_len + C::BN - 1) / C::BN;
-  hipLaunchKernelGGL((bwd_main_kernel<WAVES>), dim3(n_kvtiles * n_heads), dim3(C::THREADS), 0,
-                     stream, q, k, v, d_o, lse, delta, blockmax, d_q, d_k, d_v, n_heads, seq_len,
-                     scale, causal ? 1 : 0, pre_blocks(seq_len));
+  BwdArgs a;
+  a.Q = q;
+  a.K = k;
+  a.V = v;
+  a.dO = d_o;
+  a.LSE = lse;
+  a.delta = static_cast<const float *>(workspace);
+  a.blockmax = a.delta + ws_delta_floats(n_heads, seq_len);
+  a.dQ = d_q;
+  a.dK = d_k;
+  a.dV = d_v;
+  a.H = n_heads;
+  a.S = seq_len;
+  a.causal = causal ? 1 : 0;
+  a.n_pre_blocks = pre_blocks(seq_len);
+  a.scale = scale;
+  const int n_kv_items = n_heads * ((seq_len + kKeysPerWg - 1) / kKeysPerWg);
+  const int n_q_items = n_heads * ((seq_len + kQueriesPerWg - 1) / kQueriesPerWg);
+  hipLaunchKernelGGL(bwd_main_kernel, dim3((unsigned)(n_kv_items + n_q_items)), dim3(kThreads), 0,
+                     stream, a, n_kv_items, n_q_items);
   return hipGetLastError();
 }
 
@@ -397,7 +507,7 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
                           bool causal, hipStream_t stream) {
-  hipError_t err = launch_bwd_pre_d64(o, d_o, d_q, workspace, n_heads, seq_len, stream);
+  hipError_t err = launch_bwd_pre_d64(o, d_o, workspace, n_heads, seq_len, stream);
   if (err != hipSuccess) return err;
   return launch_bwd_main_d64(q, k, v, d_o, lse, d_q, d_k, d_v, workspace, n_heads, seq_len, scale,
                              causal, stream);

@@ -217,17 +217,17 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o, c
   return record_hip(err, "attention backward launch");
 }
 
-int dfattn_bwd_preprocess(const float *o, const float *d_o, float *d_q, void *workspace,
+int dfattn_bwd_preprocess(const float *o, const float *d_o, void *workspace,
                           size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
                           uint32_t d_head, void *stream) {
   const char *fn = "dfattn_bwd_preprocess";
   int st = check_shape(fn, n_heads, seq_len, d_head);
-  if (st == DFATTN_OK) st = check_ptrs(fn, {o, d_o, d_q});
+  if (st == DFATTN_OK) st = check_ptrs(fn, {o, d_o});
   if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
   if (st != DFATTN_OK) return st;
   // The generic kernel recomputes its row statistics itself: nothing to do.
-  if (!fast_path(d_head, {o, d_o, d_q})) return DFATTN_OK;
-  return record_hip(dfattn::launch_bwd_pre_d64(o, d_o, d_q, workspace, (int)n_heads, (int)seq_len,
+  if (!fast_path(d_head, {o, d_o})) return DFATTN_OK;
+  return record_hip(dfattn::launch_bwd_pre_d64(o, d_o, workspace, (int)n_heads, (int)seq_len,
                                                static_cast<hipStream_t>(stream)),
                     "attention backward preprocess launch");
 }

@@ -58,10 +58,92 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Max / sum over the lane pair (l, l ^ 32), the two halves of one MFMA
+// result column, with one v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// acc + sum of the 8 halves of h, accumulated in fp32 (v_dot2 with ones).
+__device__ __forceinline__ float sum8_f16(half8_t h, float acc) {
+  const half2_t one = {(half_t)1.f, (half_t)1.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(half2_t{h[2 * i], h[2 * i + 1]}, one, acc, false);
+  return acc;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
+}
+
+// ---- fp16 tiles in LDS -----------------------------------------------------
+// Every K, V, Q and dO tile the MFMA kernels stage is [rows][64] fp16 with a
+// 128-byte row stride and an XOR swizzle of its 16-byte granules: granule g of
+// row r sits at granule g ^ swz(r), swz(r) = 2*(r%4) + (r/4)%2. Two read
+// patterns use the same tile without bank conflicts (32 banks of 4 bytes):
+//  * row reads (ds_read_b128): 8 consecutive rows, one granule each;
+//  * transposed reads (ds_read_b64_tr_b16): 4 consecutive rows from a
+//    multiple of 4, two adjacent granules each.
+// and a row of 16 lanes x 8 bytes stores as one full 128-byte row.
+__device__ __forceinline__ int tile_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// Offset in halves of element (r, col), col a multiple of 4.
+__device__ __forceinline__ int tile_off(int r, int col) {
+  return r * 64 + ((((col >> 3) ^ tile_swz(r)) << 3) | (col & 7));
+}
+
+// 8 halves of row r, columns 8*g .. 8*g+7.
+__device__ __forceinline__ half8_t tile_row8(const half_t *tile, int r, int g) {
+  return *reinterpret_cast<const half8_t *>(tile + r * 64 + ((g ^ tile_swz(r)) << 3));
+}
+
+__device__ __forceinline__ void tile_store4(half_t *tile, int r, int col, float4 v) {
+  *reinterpret_cast<half4_t *>(tile + tile_off(r, col)) = to_half4(v);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) half_t lds_half_t;
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, result lane i, slot j is
+// element i%4 of the 8 bytes that lane 4*j + i/4 addresses. With lane r of
+// the group addressing (row0 + r/4, col0 + 4*(r%4)), lane i receives column
+// col0 + i of rows row0 .. row0+3 — four consecutive rows of one column.
+__device__ __forceinline__ half4_t tile_tr4(const half_t *tile, int row0, int col0, int lane) {
+  const int r = lane & 15;
+  const lds_half_t *base = (const lds_half_t *)tile;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4 *)(base + tile_off(row0 + (r >> 2), col0 + 4 * (r & 3))));
+  return __builtin_bit_cast(half4_t, v);
+}
+
+// MFMA operand (A or B) holding, for the lane's column n = 32*blk + lane%32 of
+// the tile's transpose, the 8 k-slots j -> tile rows 16*ks + 8*(j/4) + 4*hh +
+// j%4 (hh = lane/32): the row order of a 32x32 MFMA result's registers, so the
+// operand pairs with P or dS converted straight from accumulator registers.
+__device__ __forceinline__ half8_t tile_tr8(const half_t *tile, int ks, int blk, int lane) {
+  const int hh = lane >> 5, col0 = 32 * blk + 16 * ((lane >> 4) & 1);
+  const half4_t lo = tile_tr4(tile, 16 * ks + 4 * hh, col0, lane);
+  const half4_t hi = tile_tr4(tile, 16 * ks + 8 + 4 * hh, col0, lane);
+  return half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Accumulator registers (16 floats, rows 8*(r/4) + 4*hh + r%4) of two
+// consecutive 32-row blocks, as the 8 fp16 k-slots of step ks (rows
+// 16*ks + 8*(j/4) + 4*hh + j%4) — the pairing tile_tr8 reads.
+__device__ __forceinline__ half8_t acc_to_slots(const f32x16 &blk, int half_sel) {
+  const int b = 8 * half_sel;
+  half8_t h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (half_t)blk[b + j];
+  return h;
 }
 
 // ---- internal launch API (host side, all asynchronous on `stream`) -------
@@ -77,9 +159,9 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
                           bool causal, hipStream_t stream);
-// The two phases of launch_bwd_d64: Delta/dO-range/dQ:=0, then the main kernel.
-hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, float *d_q, void *workspace,
-                              int n_heads, int seq_len, hipStream_t stream);
+// The two phases of launch_bwd_d64: Delta and the dO range, then the main kernel.
+hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, void *workspace, int n_heads,
+                              int seq_len, hipStream_t stream);
 hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, const float *d_o,
                                const float *lse, float *d_q, float *d_k, float *d_v,
                                const void *workspace, int n_heads, int seq_len, float scale,

@@ -48,7 +48,7 @@ SYMBOLS = {
     "dfattn_fwd": (ctypes.c_int, [_P] * 5 + [_U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
     "dfattn_bwd": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
-    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 4 + [ctypes.c_size_t, _U32, _U32, _U32, _P]),
+    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 3 + [ctypes.c_size_t, _U32, _U32, _U32, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 9 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dfattn_last_error": (ctypes.c_int, []),
@@ -167,10 +167,10 @@ def attention_backward(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d
     return d_q, d_k, d_v
 
 
-def backward_preprocess(o, d_o, d_q, workspace, n_heads, stream=None):
-    """First phase of attention_backward (row statistics, dQ := 0)."""
+def backward_preprocess(o, d_o, workspace, n_heads, stream=None):
+    """First phase of attention_backward (row statistics Delta and the dO range)."""
     seq_len, d_head = _dims(o, n_heads)
-    _check(lib().dfattn_bwd_preprocess(_dev_ptr(o), _dev_ptr(d_o), _dev_ptr(d_q), _dev_ptr(workspace),
+    _check(lib().dfattn_bwd_preprocess(_dev_ptr(o), _dev_ptr(d_o), _dev_ptr(workspace),
                                        workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head,
                                        _stream_ptr(stream)))
 

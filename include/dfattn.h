@@ -124,14 +124,13 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o,
 
 /* The two phases of dfattn_bwd, for callers that schedule or time them
  * separately (dfattn_bwd is exactly preprocess then main, on one stream,
- * with one workspace). Preprocess reads O and dO, writes the workspace's row
- * statistics and zeroes dQ; main reads them and writes dQ, dK, dV. No
- * reference counterpart: the reference backward is one kernel without
- * saved statistics (attention_fused.cu:390-516).                            */
-int dfattn_bwd_preprocess(const float *o, const float *d_o, float *d_q,
-                          void *workspace, size_t workspace_bytes,
-                          uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
-                          void *stream);
+ * with one workspace). Preprocess reads O and dO and writes the workspace's
+ * row statistics; main reads them and writes dQ, dK, dV. No reference
+ * counterpart: the reference backward is one kernel without saved
+ * statistics (attention_fused.cu:390-516).                                  */
+int dfattn_bwd_preprocess(const float *o, const float *d_o, void *workspace,
+                          size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
+                          uint32_t d_head, void *stream);
 int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     const float *d_o, const float *lse, float *d_q, float *d_k,
                     float *d_v, void *workspace, size_t workspace_bytes,
