@@ -124,6 +124,27 @@ def summarize_pmc(fetch_csv, write_csv, copy_mib):
     return "\n".join(lines)
 
 
+def summarize_counters(counter_csv):
+    """Markdown table of any rocprofv3 --pmc run: mean counter value per dispatch, per kernel."""
+    import csv
+    import collections
+
+    acc = collections.defaultdict(list)
+    names = []
+    for r in csv.DictReader(open(counter_csv)):
+        k = short_kernel_name(r["Kernel_Name"])
+        if k in KERNELS:
+            acc[(k, r["Counter_Name"])].append(float(r["Counter_Value"]))
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+    lines = ["| kernel | " + " | ".join(names) + " |", "|---" * (len(names) + 1) + "|"]
+    for k in KERNELS:
+        vals = [acc.get((k, c)) for c in names]
+        if any(vals):
+            lines.append(f"| {k} | " + " | ".join(f"{sum(v) / len(v):.4g}" if v else "-" for v in vals) + " |")
+    return "\n".join(lines)
+
+
 def summarize_trace(stats_csv):
     """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
     import csv
@@ -142,6 +163,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-heads", type=int, default=6, help="heads in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--gpt2-steps", type=int, default=10,
+                    help="timed GPT-2 small training steps at S=1024 (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run 5 plain device copies of MIB MiB each (the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -149,12 +172,17 @@ def main():
                     help="print the HBM-traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
                     help="print a rocprofv3 --kernel-trace --stats summary table and exit (no GPU)")
+    ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
+                    help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.copy_calibration or 512))
         return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -246,6 +274,21 @@ def main():
         "roofline": roofline,
         "gpt2_step_ms": None,
     }
+    if args.gpt2_steps > 0:
+        from dfattn.gpt2_step import StaticGPT2, time_steps
+
+        log(f"GPT-2 small step (S=1024), {args.gpt2_steps} timed steps")
+        model = StaticGPT2(seq_len=1024, seed=0)
+        g2 = time_steps(model, steps=args.gpt2_steps, warmup=3)
+        result["gpt2_step_ms"] = round(g2["median_ms"], 3)
+        result["gpt2_step"] = {"config": "12 layers, d_model 768, 12 heads, d_ff 3072, vocab 50257, S=1024, batch 1",
+                               "weights": "fp32, N(0,0.02) seeded", "tokens": "uniform [0,50257) seeded",
+                               "median_ms": round(g2["median_ms"], 3), "min_ms": round(g2["min_ms"], 3),
+                               "steps": args.gpt2_steps, "warmup": 3,
+                               "loss_first": round(g2["losses"][0], 4), "loss_last": round(g2["losses"][-1], 4),
+                               "peak_mem_mb": round(g2["peak_mem_mb"], 1)}
+        del model
+        log(f"GPT-2 step median {g2['median_ms']:.2f} ms")
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.randn(n, device=dev)

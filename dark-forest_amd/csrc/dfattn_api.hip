@@ -12,19 +12,36 @@
 
 #include "dfattn.h"
 #include "dfattn_internal.h"
+#include "dfattn_status.h"
 
 namespace {
-
 std::mutex g_err_mu;
-int g_err = DFATTN_OK;
+int g_err = DFATTN_OK;  // last error of any entry point (dfattn_last_error)
 std::string g_err_msg;
+// First error of a reference launcher symbol (void return, no other way to
+// report) since the last darkforest_sync, which aborts on it.
+int g_pending = DFATTN_OK;
+std::string g_pending_msg;
 
-int record_error(int status, const std::string &msg) {
+void mark_pending_if_failed(int status) {
+  if (status == DFATTN_OK) return;
+  std::lock_guard<std::mutex> lock(g_err_mu);
+  if (g_pending == DFATTN_OK) {
+    g_pending = status;
+    g_pending_msg = g_err_msg;
+  }
+}
+}  // namespace
+
+int dfattn::record_error(int status, const std::string &msg) {
   std::lock_guard<std::mutex> lock(g_err_mu);
   g_err = status;
   g_err_msg = msg;
   return status;
 }
+
+namespace {
+using dfattn::record_error;
 
 int record_hip(hipError_t err, const char *where) {
   if (err == hipSuccess) return DFATTN_OK;
@@ -82,12 +99,13 @@ int fwd_impl(const float *q, const float *k, const float *v, float *o, float *ls
 // Legacy backward: the caller's probability scratch (`capacity` floats) holds
 // O, lse and the fast path's workspace when it is large enough; otherwise the
 // self-contained generic kernel runs.
-void legacy_backward(const char *fn, const float *q, const float *k, const float *v,
-                     const float *d_out, float *d_q, float *d_k, float *d_v, float *scratch,
-                     size_t capacity, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
-                     float scale, uint32_t causal) {
-  if (check_shape(fn, n_heads, seq_len, d_head) != DFATTN_OK) return;
-  if (check_ptrs(fn, {q, k, v, d_out, d_q, d_k, d_v}) != DFATTN_OK) return;
+int legacy_backward(const char *fn, const float *q, const float *k, const float *v,
+                    const float *d_out, float *d_q, float *d_k, float *d_v, float *scratch,
+                    size_t capacity, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                    float scale, uint32_t causal) {
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, d_out, d_q, d_k, d_v});
+  if (st != DFATTN_OK) return st;
   const size_t elems = (size_t)seq_len * n_heads * d_head;
   const size_t lse_floats = ((size_t)n_heads * seq_len + 63) / 64 * 64;
   const size_t ws_floats = dfattn::bwd_workspace_bytes_d64((int)n_heads, (int)seq_len) / sizeof(float);
@@ -106,7 +124,7 @@ void legacy_backward(const char *fn, const float *q, const float *k, const float
     err = dfattn::launch_bwd_generic(q, k, v, d_out, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
                                      (int)d_head, scale, causal != 0, nullptr);
   }
-  record_hip(err, fn);
+  return record_hip(err, fn);
 }
 
 }  // namespace
@@ -118,18 +136,21 @@ extern "C" {
 void launch_fused_attention(const float *q, const float *k, const float *v, float *out,
                             uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal) {
   const char *fn = "launch_fused_attention";
-  if (check_shape(fn, 1, seq_len, d_head) != DFATTN_OK) return;
-  if (check_ptrs(fn, {q, k, v, out}) != DFATTN_OK) return;
-  fwd_impl(q, k, v, out, nullptr, 1, seq_len, d_head, scale, causal, nullptr);
+  int st = check_shape(fn, 1, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, out});
+  if (st == DFATTN_OK) st = fwd_impl(q, k, v, out, nullptr, 1, seq_len, d_head, scale, causal, nullptr);
+  mark_pending_if_failed(st);
 }
 
 void launch_fused_mha_forward(const float *q, const float *k, const float *v, float *out,
                               uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale,
                               uint32_t causal) {
   const char *fn = "launch_fused_mha_forward";
-  if (check_shape(fn, n_heads, seq_len, d_head) != DFATTN_OK) return;
-  if (check_ptrs(fn, {q, k, v, out}) != DFATTN_OK) return;
-  fwd_impl(q, k, v, out, nullptr, n_heads, seq_len, d_head, scale, causal, nullptr);
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, out});
+  if (st == DFATTN_OK)
+    st = fwd_impl(q, k, v, out, nullptr, n_heads, seq_len, d_head, scale, causal, nullptr);
+  mark_pending_if_failed(st);
 }
 
 void launch_attention_backward(const float *q, const float *k, const float *v,
@@ -137,8 +158,9 @@ void launch_attention_backward(const float *q, const float *k, const float *v,
                                float *probabilities, uint32_t seq_len, uint32_t d_head,
                                float scale, uint32_t causal) {
   // Scratch is [seq_len, seq_len] (lib.rs:2441).
-  legacy_backward("launch_attention_backward", q, k, v, d_out, d_q, d_k, d_v, probabilities,
-                  (size_t)seq_len * seq_len, 1, seq_len, d_head, scale, causal);
+  mark_pending_if_failed(legacy_backward("launch_attention_backward", q, k, v, d_out, d_q, d_k,
+                                         d_v, probabilities, (size_t)seq_len * seq_len, 1,
+                                         seq_len, d_head, scale, causal));
 }
 
 void launch_fused_mha_backward(const float *q, const float *k, const float *v,
@@ -146,8 +168,10 @@ void launch_fused_mha_backward(const float *q, const float *k, const float *v,
                                float *probabilities, uint32_t n_heads, uint32_t seq_len,
                                uint32_t d_head, float scale, uint32_t causal) {
   // Scratch is [n_heads, 2, seq_len, seq_len] (lib.rs:2023).
-  legacy_backward("launch_fused_mha_backward", q, k, v, d_out, d_q, d_k, d_v, probabilities,
-                  (size_t)n_heads * 2 * seq_len * seq_len, n_heads, seq_len, d_head, scale, causal);
+  mark_pending_if_failed(legacy_backward("launch_fused_mha_backward", q, k, v, d_out, d_q, d_k,
+                                         d_v, probabilities,
+                                         (size_t)n_heads * 2 * seq_len * seq_len, n_heads, seq_len,
+                                         d_head, scale, causal));
 }
 
 void darkforest_sync(void) {
@@ -157,9 +181,9 @@ void darkforest_sync(void) {
     abort();
   }
   std::lock_guard<std::mutex> lock(g_err_mu);
-  if (g_err != DFATTN_OK) {
+  if (g_pending != DFATTN_OK) {
     fprintf(stderr, "[darkforest] attention launch error before sync boundary: %s\n",
-            g_err_msg.c_str());
+            g_pending_msg.c_str());
     abort();
   }
 }
@@ -282,6 +306,8 @@ void dfattn_clear_error(void) {
   std::lock_guard<std::mutex> lock(g_err_mu);
   g_err = DFATTN_OK;
   g_err_msg.clear();
+  g_pending = DFATTN_OK;
+  g_pending_msg.clear();
 }
 
 const char *dfattn_version(void) { return "dfattn 0.1.0 (gfx950, MFMA f16 / fp32 accumulate)"; }

@@ -10,7 +10,8 @@ The library's C ABI is include/dfattn.h. This module loads the in-tree build
   pointers and torch's current HIP stream;
 * ``AttentionContext``, the mirror of the reference's per-layer context
   (darkforest-cuda/src/lib.rs:1949-2368), and the host-slice helpers
-  ``fused_attention_forward`` / ``attention_backward`` (lib.rs:2371, 2421).
+  ``fused_attention_forward`` / ``attention_backward_host`` (lib.rs:2371, 2421);
+* ``FusedCausalAttention``, a torch.autograd.Function over the fast path.
 
 There is no CPU fallback: if the library is missing every call raises
 ``DfattnNotBuilt``.
@@ -55,6 +56,18 @@ SYMBOLS = {
     "dfattn_last_error_message": (ctypes.c_char_p, []),
     "dfattn_clear_error": (None, []),
     "dfattn_version": (ctypes.c_char_p, []),
+    "dfattn_context_create": (ctypes.c_int, [_U32, _U32, _U32, ctypes.POINTER(ctypes.c_void_p)]),
+    "dfattn_context_destroy": (None, [_P]),
+    "dfattn_context_dims": (ctypes.c_int, [_P] + [ctypes.POINTER(_U32)] * 4),
+    "dfattn_context_lse": (_P, [_P]),
+    "dfattn_context_forward_device_into": (ctypes.c_int, [_P] * 4 + [_F, _U32, _P, ctypes.c_size_t, _P]),
+    "dfattn_context_backward_device_into": (ctypes.c_int,
+                                            [_P] * 5 + [_F, _U32, _P, _P, _P, ctypes.c_size_t, _P]),
+    "dfattn_context_forward": (ctypes.c_int, [_P] * 4 + [ctypes.c_size_t, _F, _U32, _P]),
+    "dfattn_context_backward": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _F, _U32, _P, _P, _P]),
+    "dfattn_fused_attention_forward": (ctypes.c_int, [_P] * 3 + [ctypes.c_size_t, _U32, _U32, _F, _U32, _P]),
+    "dfattn_attention_backward": (ctypes.c_int,
+                                  [_P] * 4 + [ctypes.c_size_t, _U32, _U32, _F, _U32, _P, _P, _P]),
 }
 
 
@@ -217,3 +230,156 @@ def darkforest_sync():
     """matmul.cu:21: device synchronize; aborts the process on error."""
     lib().darkforest_sync()
 
+
+
+# ---------------------------------------------------------------- the reference's context
+def _host_f32(a, name, n):
+    import numpy as np
+
+    arr = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    if arr.size != n:
+        raise DfattnError(-3, f"{name} must have {n} elements, got {arr.size}")
+    return arr
+
+
+class AttentionContext:
+    """Mirror of the reference's per-layer AttentionContext (darkforest-cuda/src/lib.rs:1949-2368).
+
+    ``AttentionContext(n_heads, seq_len, d_head)`` validates like ``new_shared``
+    (lib.rs:1975-1989) and allocates its logsumexp and backward workspace up
+    front. Device-path methods take torch device tensors of shape
+    [seq_len, n_heads * d_head]; host-slice methods take array-likes of
+    seq_len * d_head floats and run one head, as the reference's do.
+    """
+
+    def __init__(self, n_heads, seq_len, d_head):
+        handle = ctypes.c_void_p()
+        _check(lib().dfattn_context_create(n_heads, seq_len, d_head, ctypes.byref(handle)))
+        self._h = handle
+        self.n_heads, self.seq_len, self.d_head = n_heads, seq_len, d_head
+        self.d_model = n_heads * d_head
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().dfattn_context_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _elems(self, t):
+        if tuple(t.shape) != (self.seq_len, self.d_model):
+            return -1
+        return t.numel()
+
+    def forward_device_into(self, q, k, v, scale, causal, out, stream=None):
+        """lib.rs:2042: O into `out`; also the context's logsumexp."""
+        _check(lib().dfattn_context_forward_device_into(
+            self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), scale, int(bool(causal)), _dev_ptr(out),
+            self._elems(out) & ((1 << 64) - 1), _stream_ptr(stream)))
+
+    def forward_device(self, q, k, v, scale, causal, stream=None):
+        """lib.rs:2029: allocate O and run forward_device_into."""
+        out = _torch().empty((self.seq_len, self.d_model), dtype=q.dtype, device=q.device)
+        self.forward_device_into(q, k, v, scale, causal, out, stream)
+        return out
+
+    def backward_device_into(self, q, k, v, d_out, scale, causal, d_q, d_k, d_v, stream=None):
+        """lib.rs:2240: dQ, dK, dV into the given tensors."""
+        n = min(self._elems(d_q), self._elems(d_k), self._elems(d_v))
+        _check(lib().dfattn_context_backward_device_into(
+            self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(d_out), scale, int(bool(causal)),
+            _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), n & ((1 << 64) - 1), _stream_ptr(stream)))
+
+    def backward_device(self, q, k, v, d_out, scale, causal, stream=None):
+        """lib.rs:2226: allocate dQ, dK, dV and run backward_device_into."""
+        torch = _torch()
+        grads = [torch.empty((self.seq_len, self.d_model), dtype=q.dtype, device=q.device) for _ in range(3)]
+        self.backward_device_into(q, k, v, d_out, scale, causal, *grads, stream=stream)
+        return tuple(grads)
+
+    def forward(self, q, k, v, scale, causal):
+        """lib.rs:2295: host slices [seq_len * d_head] in, host O out."""
+        import numpy as np
+
+        n = self.seq_len * self.d_head
+        arrs = [_host_f32(a, name, n) for a, name in ((q, "q"), (k, "k"), (v, "v"))]
+        out = np.empty(n, dtype=np.float32)
+        _check(lib().dfattn_context_forward(self._h, *(a.ctypes.data for a in arrs), n, scale, int(bool(causal)),
+                                            out.ctypes.data))
+        return out
+
+    def backward(self, d_out, scale, causal):
+        """lib.rs:2328: host dO in, host (dQ, dK, dV) out, for the last host forward's q, k, v."""
+        import numpy as np
+
+        n = self.seq_len * self.d_head
+        g = _host_f32(d_out, "d_out", n)
+        outs = [np.empty(n, dtype=np.float32) for _ in range(3)]
+        _check(lib().dfattn_context_backward(self._h, g.ctypes.data, n, scale, int(bool(causal)),
+                                             *(o.ctypes.data for o in outs)))
+        return tuple(outs)
+
+
+def fused_attention_forward(q, k, v, seq_len, d_head, scale, causal):
+    """lib.rs:2371: one head from host slices; returns host O [seq_len * d_head]."""
+    import numpy as np
+
+    n = seq_len * d_head
+    arrs = [_host_f32(a, name, n) for a, name in ((q, "q"), (k, "k"), (v, "v"))]
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().dfattn_fused_attention_forward(*(a.ctypes.data for a in arrs), n, seq_len, d_head, scale,
+                                                int(bool(causal)), out.ctypes.data))
+    return out
+
+
+def attention_backward_host(q, k, v, d_out, seq_len, d_head, scale, causal):
+    """lib.rs:2421 attention_backward: one head from host slices; returns host (dQ, dK, dV)."""
+    import numpy as np
+
+    n = seq_len * d_head
+    arrs = [_host_f32(a, name, n) for a, name in ((q, "q"), (k, "k"), (v, "v"), (d_out, "d_out"))]
+    outs = [np.empty(n, dtype=np.float32) for _ in range(3)]
+    _check(lib().dfattn_attention_backward(*(a.ctypes.data for a in arrs), n, seq_len, d_head, scale,
+                                           int(bool(causal)), *(o.ctypes.data for o in outs)))
+    return tuple(outs)
+
+
+class FusedCausalAttention:
+    """torch.autograd.Function over the fast path (the role of the reference's
+    CudaAttentionGradFn, darkforest-core/src/autograd/grad_fn.rs:23-57).
+
+    ``FusedCausalAttention.apply(q, k, v, n_heads, scale, causal)`` with q, k, v
+    [S, H*D] float32 device tensors; the backward reuses the forward's O and
+    logsumexp.
+    """
+
+    _fn = None
+
+    @classmethod
+    def apply(cls, q, k, v, n_heads, scale=None, causal=True):
+        if cls._fn is None:
+            torch = _torch()
+
+            class _Fn(torch.autograd.Function):
+                @staticmethod
+                def forward(ctx, q, k, v, n_heads, scale, causal):
+                    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+                    o, lse = attention_forward(q, k, v, n_heads, scale, causal)
+                    ctx.save_for_backward(q, k, v, o, lse)
+                    ctx.n_heads, ctx.scale, ctx.causal = n_heads, scale, causal
+                    return o
+
+                @staticmethod
+                def backward(ctx, d_o):
+                    q, k, v, o, lse = ctx.saved_tensors
+                    dq, dk, dv = attention_backward(q, k, v, o, d_o.contiguous(), lse, ctx.n_heads, ctx.scale,
+                                                    ctx.causal)
+                    return dq, dk, dv, None, None, None
+
+            cls._fn = _Fn
+        d_head = q.shape[1] // n_heads
+        return cls._fn.apply(q, k, v, n_heads, d_head ** -0.5 if scale is None else scale, causal)

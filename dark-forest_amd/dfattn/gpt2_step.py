@@ -1,0 +1,162 @@
+"""GPT-2 training step around the fused attention: the harness that reports "GPT-2 step ms".
+
+Mirrors the reference's static engine step (darkforest-core/src/engine/static_gpt2.rs):
+
+* model (static_gpt2.rs:276-567): learned token and position embeddings, L
+  pre-LayerNorm blocks (LN eps 1e-5, darkforest-cuda/kernels/layernorm.cu:14),
+  Q/K/V/O projections with biases, tanh-GELU MLP (elementwise.cu:181-192),
+  final LayerNorm and an untied lm_head [vocab, d_model];
+* initialisation (static_gpt2.rs:285-319): weights N(0, 0.02), the residual
+  projections Wo and W2 N(0, 0.02 / sqrt(2 L)), LayerNorm gamma 1 / beta 0,
+  biases 0 — drawn from a seeded generator (the reference's thread_rng is
+  unseeded, static_gpt2.rs:264-271);
+* step (static_gpt2.rs:1375-1696): forward, mean cross-entropy over the S
+  positions, backward, AdamW with beta (0.9, 0.95), eps 1e-8 and weight decay
+  0.1 on every parameter (static_gpt2.rs:518-521; update rule lib.rs:1755-1788);
+* attention: per layer the fused causal kernel with scale (d_model/H)^-0.5
+  (static_gpt2.rs:1291, 1329-1336, 1500-1510) — here dfattn's fast path through
+  FusedCausalAttention, which keeps the forward's O and logsumexp for the
+  backward.
+
+Everything except attention is plain PyTorch in fp32 (GEMMs through
+hipBLASLt/rocBLAS); it is the measurement harness of the attention path, not
+a reimplementation of the reference's other kernels. `attention="sdpa"`
+swaps in torch's scaled_dot_product_attention (the reference's own parity
+comparator, scripts/verify_loss_parity.py:58) for loss-parity checks.
+"""
+from __future__ import annotations
+
+import math
+import time
+
+from . import FusedCausalAttention
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+class StaticGPT2:
+    """GPT-2 with the reference engine's architecture, init and optimizer."""
+
+    def __init__(self, vocab_size=50257, d_model=768, n_heads=12, n_layers=12, d_ff=3072, seq_len=1024, lr=3e-4,
+                 seed=0, device="cuda", attention="dfattn"):
+        torch = _torch()
+        if d_model % n_heads:
+            raise ValueError("d_model must be divisible by n_heads")
+        if d_model // n_heads > 128:
+            raise ValueError(f"StaticGPT2 head dimension must be <= 128, got {d_model // n_heads}")
+        if attention not in ("dfattn", "sdpa"):
+            raise ValueError("attention must be 'dfattn' or 'sdpa'")
+        self.vocab_size, self.d_model, self.n_heads = vocab_size, d_model, n_heads
+        self.n_layers, self.d_ff, self.seq_len = n_layers, d_ff, seq_len
+        self.attention = attention
+        self.device = torch.device(device)
+        gen = torch.Generator(device="cpu").manual_seed(seed)
+        std, std_res = 0.02, 0.02 / math.sqrt(2.0 * n_layers)
+
+        def randn(*shape, s=std):
+            return (torch.randn(*shape, generator=gen) * s).to(self.device).requires_grad_(True)
+
+        def const(v, *shape):
+            return torch.full(shape, float(v), device=self.device).requires_grad_(True)
+
+        self.tok_emb = randn(vocab_size, d_model)
+        self.pos_emb = randn(seq_len, d_model)
+        self.layers = []
+        for _ in range(n_layers):
+            self.layers.append({
+                "ln1_g": const(1, d_model), "ln1_b": const(0, d_model),
+                "wq": randn(d_model, d_model), "bq": const(0, d_model),
+                "wk": randn(d_model, d_model), "bk": const(0, d_model),
+                "wv": randn(d_model, d_model), "bv": const(0, d_model),
+                "wo": randn(d_model, d_model, s=std_res), "bo": const(0, d_model),
+                "ln2_g": const(1, d_model), "ln2_b": const(0, d_model),
+                "w1": randn(d_ff, d_model), "b1": const(0, d_ff),
+                "w2": randn(d_model, d_ff, s=std_res), "b2": const(0, d_model),
+            })
+        self.ln_f_g = const(1, d_model)
+        self.ln_f_b = const(0, d_model)
+        self.lm_head = randn(vocab_size, d_model)
+        self.opt = torch.optim.AdamW(self.parameters(), lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        self.pos_idx = torch.arange(seq_len, device=self.device)
+
+    def parameters(self):
+        ps = [self.tok_emb, self.pos_emb]
+        for lw in self.layers:
+            ps += list(lw.values())
+        return ps + [self.ln_f_g, self.ln_f_b, self.lm_head]
+
+    def load_state(self, other: "StaticGPT2"):
+        """Copy another instance's weights (the parity harness loads identical weights into both)."""
+        torch = _torch()
+        with torch.no_grad():
+            for a, b in zip(self.parameters(), other.parameters()):
+                a.copy_(b)
+
+    def _attention(self, q, k, v):
+        torch = _torch()
+        scale = (self.d_model / self.n_heads) ** -0.5
+        if self.attention == "dfattn":
+            return FusedCausalAttention.apply(q, k, v, self.n_heads, scale, True)
+        s, h, d = q.shape[0], self.n_heads, self.d_model // self.n_heads
+        qh, kh, vh = (t.view(s, h, d).transpose(0, 1).contiguous() for t in (q, k, v))
+        o = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
+        return o.transpose(0, 1).reshape(s, h * d)
+
+    def loss(self, tokens, targets):
+        """Mean cross-entropy of one sequence (static_gpt2.rs:1386-1418)."""
+        F = _torch().nn.functional
+        x = self.tok_emb[tokens] + self.pos_emb[self.pos_idx]
+        for lw in self.layers:
+            h = F.layer_norm(x, (self.d_model,), lw["ln1_g"], lw["ln1_b"], 1e-5)
+            q = F.linear(h, lw["wq"], lw["bq"])
+            k = F.linear(h, lw["wk"], lw["bk"])
+            v = F.linear(h, lw["wv"], lw["bv"])
+            x = x + F.linear(self._attention(q, k, v), lw["wo"], lw["bo"])
+            h = F.layer_norm(x, (self.d_model,), lw["ln2_g"], lw["ln2_b"], 1e-5)
+            x = x + F.linear(F.gelu(F.linear(h, lw["w1"], lw["b1"]), approximate="tanh"), lw["w2"], lw["b2"])
+        h = F.layer_norm(x, (self.d_model,), self.ln_f_g, self.ln_f_b, 1e-5)
+        return F.cross_entropy(F.linear(h, self.lm_head), targets)
+
+    def step(self, tokens, targets):
+        """One training step: forward, loss, backward, AdamW. Returns the loss tensor (not synchronised)."""
+        self.opt.zero_grad(set_to_none=False)
+        loss = self.loss(tokens, targets)
+        loss.backward()
+        self.opt.step()
+        return loss.detach()
+
+
+def synthetic_batch(vocab_size, seq_len, seed, device):
+    """Token ids and next-token targets uniform in [0, vocab) from a seeded generator."""
+    torch = _torch()
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    ids = torch.randint(0, vocab_size, (seq_len + 1,), generator=gen)
+    return ids[:-1].to(device), ids[1:].to(device)
+
+
+def time_steps(model, steps=10, warmup=3, seed=1):
+    """Median and all per-step wall times (ms) of full training steps, device-synchronised per step.
+
+    The methodology of the reference's step benchmark (benchmark/bench_darkforest_e2e.py:116-133:
+    warmup, then timed steps each ending in a device sync), with seeded tokens.
+    """
+    torch = _torch()
+    tokens, targets = synthetic_batch(model.vocab_size, model.seq_len, seed, model.device)
+    losses = []
+    for _ in range(warmup):
+        losses.append(float(model.step(tokens, targets)))
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        loss = model.step(tokens, targets)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+        losses.append(float(loss))
+    ordered = sorted(times)
+    return {"median_ms": ordered[len(ordered) // 2], "min_ms": ordered[0], "times_ms": times, "losses": losses,
+            "peak_mem_mb": torch.cuda.max_memory_allocated() / 2 ** 20}

@@ -89,8 +89,10 @@ void launch_fused_mha_backward(const float *q, const float *k, const float *v,
                                uint32_t n_heads, uint32_t seq_len,
                                uint32_t d_head, float scale, uint32_t causal);
 
-/* matmul.cu:21 — device synchronize; on any recorded or HIP error print
- * "[darkforest] ..." to stderr and abort(), as the reference does.         */
+/* matmul.cu:21 — device synchronize; on a HIP error, or on an argument
+ * error of one of the four launchers above since the last sync, print
+ * "[darkforest] ..." to stderr and abort(), as the reference does. Errors
+ * the status-returning entry points below already returned do not abort.   */
 void darkforest_sync(void);
 
 /* ---- Group 2: fast path -------------------------------------------------
@@ -137,11 +139,70 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                     float scale, uint32_t causal, void *stream);
 
+/* ---- Group 3: the reference's per-layer attention context ---------------
+ * Mirror of AttentionContext (darkforest-cuda/src/lib.rs:1949-2368), the
+ * object each layer of the reference's static GPT-2 engine owns
+ * (static_gpt2.rs:401-406). All device buffers it needs (logsumexp [H, S]
+ * and the backward workspace, O(H*S)) are allocated by create; the reference
+ * instead allocates an H*2*S*S scratch on the first backward (lib.rs:2019).
+ * The context is internally locked, like the reference's Mutex fields.    */
+typedef struct dfattn_context dfattn_context;
+
+/* lib.rs:1966 AttentionContext::new (and :1975 new_shared): d_head in
+ * 1..=128, n_heads*d_head and seq_len*d_model must not overflow.            */
+int dfattn_context_create(uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                          dfattn_context **out);
+void dfattn_context_destroy(dfattn_context *ctx);
+int dfattn_context_dims(const dfattn_context *ctx, uint32_t *n_heads, uint32_t *seq_len,
+                        uint32_t *d_head, uint32_t *d_model);
+/* The context's logsumexp buffer [n_heads, seq_len], written by every
+ * forward (device pointer; NULL for a NULL context).                        */
+const float *dfattn_context_lse(const dfattn_context *ctx);
+
+/* lib.rs:2042 forward_device_into: O [seq_len, d_model] from device Q, K, V;
+ * out_elems must equal seq_len * d_model ("attention output shape
+ * mismatch"). Also writes the context's logsumexp and remembers q, k, v and
+ * out for the backward.                                                     */
+int dfattn_context_forward_device_into(dfattn_context *ctx, const float *q, const float *k,
+                                       const float *v, float scale, uint32_t causal,
+                                       float *out, size_t out_elems, void *stream);
+
+/* lib.rs:2240 backward_device_into: dQ, dK, dV (each seq_len * d_model =
+ * grad_elems). Uses the O and logsumexp of the last forward_device_into on
+ * the same q, k, v, scale and causal (the caller keeps that O unmodified in
+ * between, as the reference engine does, static_gpt2.rs:1329-1336,
+ * 1500-1510); otherwise recomputes them first.                              */
+int dfattn_context_backward_device_into(dfattn_context *ctx, const float *q, const float *k,
+                                        const float *v, const float *d_out, float scale,
+                                        uint32_t causal, float *d_q, float *d_k, float *d_v,
+                                        size_t grad_elems, void *stream);
+
+/* lib.rs:2295 forward / :2328 backward: host slices of seq_len * d_head
+ * floats uploaded into context buffers and run on the single-head path, as
+ * the reference does; backward differentiates the last host forward's
+ * q, k, v. Synchronous.                                                     */
+int dfattn_context_forward(dfattn_context *ctx, const float *q, const float *k, const float *v,
+                           size_t len, float scale, uint32_t causal, float *out);
+int dfattn_context_backward(dfattn_context *ctx, const float *d_out, size_t len, float scale,
+                            uint32_t causal, float *d_q, float *d_k, float *d_v);
+
+/* lib.rs:2371 fused_attention_forward and :2421 attention_backward: one
+ * head [seq_len, d_head] from host slices through device buffers allocated
+ * for the call. Synchronous.                                                */
+int dfattn_fused_attention_forward(const float *q, const float *k, const float *v, size_t len,
+                                   uint32_t seq_len, uint32_t d_head, float scale,
+                                   uint32_t causal, float *out);
+int dfattn_attention_backward(const float *q, const float *k, const float *v,
+                              const float *d_out, size_t len, uint32_t seq_len,
+                              uint32_t d_head, float scale, uint32_t causal, float *d_q,
+                              float *d_k, float *d_v);
+
 /* Human-readable name of a dfattn_status value.                             */
 const char *dfattn_status_string(int status);
 
 /* The last error recorded by any entry point of this library on any thread
- * (0 if none), and a message for it; dfattn_clear_error() resets it.       */
+ * (0 if none), and a message for it; dfattn_clear_error() resets it and the
+ * launcher error darkforest_sync() would report.                          */
 int dfattn_last_error(void);
 const char *dfattn_last_error_message(void);
 void dfattn_clear_error(void);

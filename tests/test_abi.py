@@ -124,3 +124,57 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(dfattn, "LIB_PATH", str(tmp_path / "libdfattn.so"))
     with pytest.raises(dfattn.DfattnNotBuilt):
         dfattn.lib()
+
+
+# ---------------------------------------------------------------- the context mirror (lib.rs:1949-2368)
+@pytest.mark.parametrize("dims,status", [
+    ((12, 128, 0), -4), ((12, 128, 129), -4), ((0, 128, 64), -3), ((12, 0, 64), -3),
+    ((2 ** 32 - 1, 2 ** 32 - 1, 128), -5),
+])
+def test_context_create_validates_like_new_shared(dims, status):
+    """AttentionContext::new_shared's checks (lib.rs:1981-1989) run before any device allocation."""
+    lib = dfattn.lib()
+    handle = ctypes.c_void_p(0x1234)
+    assert lib.dfattn_context_create(*dims, ctypes.byref(handle)) == status
+    assert handle.value is None  # out-pointer cleared on failure
+    assert lib.dfattn_last_error() == status
+
+
+def test_context_create_rejects_null_out_pointer():
+    assert dfattn.lib().dfattn_context_create(12, 128, 64, None) == -1
+
+
+def test_null_context_calls_fail_cleanly():
+    lib = dfattn.lib()
+    assert lib.dfattn_context_forward_device_into(None, FAKE, FAKE, FAKE, 0.125, 1, FAKE, 10, None) == -1
+    assert lib.dfattn_context_backward_device_into(None, FAKE, FAKE, FAKE, FAKE, 0.125, 1, FAKE, FAKE, FAKE, 10,
+                                                   None) == -1
+    assert lib.dfattn_context_lse(None) is None
+    lib.dfattn_context_destroy(None)  # no-op
+
+
+def test_host_helpers_reject_bad_shapes_before_allocating():
+    """fused_attention_forward / attention_backward (lib.rs:2371-2479) shape errors."""
+    import numpy as np
+
+    with pytest.raises(dfattn.DfattnError) as e:
+        dfattn.fused_attention_forward(np.zeros(10), np.zeros(10), np.zeros(10), 5, 3, 0.5, True)
+    assert e.value.status == -3
+    lib = dfattn.lib()
+    buf = (ctypes.c_float * 16)()
+    assert lib.dfattn_fused_attention_forward(buf, buf, buf, 15, 4, 4, 0.5, 1, buf) == -3
+    assert lib.dfattn_fused_attention_forward(buf, buf, buf, 16, 4, 0, 0.5, 1, buf) == -4
+    assert lib.dfattn_attention_backward(buf, buf, buf, buf, 15, 4, 4, 0.5, 1, buf, buf, buf) == -3
+    assert b"[seq_len, d_head]" in lib.dfattn_last_error_message()
+
+
+def test_context_error_is_returned_and_recorded_in_a_fresh_process():
+    """A context error comes back as a status and is readable through dfattn_last_error."""
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path.insert(0, %r); import ctypes, dfattn; lib = dfattn.lib(); "
+            "h = ctypes.c_void_p(); assert lib.dfattn_context_create(12, 128, 0, ctypes.byref(h)) == -4; "
+            "assert lib.dfattn_last_error() == -4; print('ok')") % os.path.join(ROOT, "dark-forest_amd")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and "ok" in out.stdout, out.stderr
