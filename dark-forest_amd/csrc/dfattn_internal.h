@@ -17,6 +17,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Word 3 of a raw buffer descriptor (gfx9 family: 32-bit data format, no
+// swizzle); loads past num_records return zeros.
+constexpr int kBufferFlags = 0x00020000;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // D = 64 fast path: one 32x32x16 fp16 MFMA (fp32 accumulate). Operand
@@ -86,13 +89,18 @@ __device__ __forceinline__ float wave_max(float v) {
 // ---- fp16 tiles in LDS -----------------------------------------------------
 // Every K, V, Q and dO tile the MFMA kernels stage is [rows][64] fp16 with a
 // 128-byte row stride and an XOR swizzle of its 16-byte granules: granule g of
-// row r sits at granule g ^ swz(r), swz(r) = 2*(r%4) + (r/4)%2. Two read
-// patterns use the same tile without bank conflicts (32 banks of 4 bytes):
-//  * row reads (ds_read_b128): 8 consecutive rows, one granule each;
-//  * transposed reads (ds_read_b64_tr_b16): 4 consecutive rows from a
-//    multiple of 4, two adjacent granules each.
-// and a row of 16 lanes x 8 bytes stores as one full 128-byte row.
-__device__ __forceinline__ int tile_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// row r sits at granule g ^ swz(r), swz(r) = 4*((r/2)%2) + (r/4)%4. The LDS
+// has 64 banks of 4 bytes, so rows r and r+1 fill one 256-byte bank line.
+// The three access patterns of the kernels are conflict-free:
+//  * row reads (ds_read_b128, 16 lanes per pass): 16 consecutive rows from a
+//    multiple of 16, one granule each — even rows take 8 distinct granules
+//    and so do odd rows;
+//  * transposed reads (ds_read_b64_tr_b16, 32 lanes per pass): 4 consecutive
+//    rows from a multiple of 4, four adjacent granules each — rows r and r+2
+//    differ in bit 2 of the swizzle, which moves an aligned group of four
+//    granules to the other group;
+//  * stores (8 bytes per lane, 32 lanes per pass): two full rows.
+__device__ __forceinline__ int tile_swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
 
 // Offset in halves of element (r, col), col a multiple of 4.
 __device__ __forceinline__ int tile_off(int r, int col) {
@@ -122,6 +130,18 @@ __device__ __forceinline__ half4_t tile_tr4(const half_t *tile, int row0, int co
   const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_i16x4 *)(base + tile_off(row0 + (r >> 2), col0 + 4 * (r & 3))));
   return __builtin_bit_cast(half4_t, v);
+}
+
+// Offset (in halves) that tile_tr4 reads for this lane, and the read itself
+// at a precomputed offset: loops keep the offsets in registers and add only
+// the stage base.
+__device__ __forceinline__ int tile_tr4_off(int row0, int col0, int lane) {
+  const int r = lane & 15;
+  return tile_off(row0 + (r >> 2), col0 + 4 * (r & 3));
+}
+__device__ __forceinline__ half4_t tile_tr4_at(const half_t *tile, int off) {
+  const lds_half_t *base = (const lds_half_t *)tile;
+  return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(base + off)));
 }
 
 // MFMA operand (A or B) holding, for the lane's column n = 32*blk + lane%32 of
