@@ -30,6 +30,8 @@
 //
 #include "dfattn_internal.h"
 
+#include <type_traits>
+
 namespace dfattn {
 namespace {
 
@@ -102,9 +104,18 @@ constexpr int kKTile = 64;          // dQ workgroup: keys per step (2 halves of 
 constexpr int kTile = 64 * kD;      // halves per staged [64][64] tile
 constexpr int kStageF4 = 64 * kD / 4 / kThreads;  // float4 per thread per staged tile
 static_assert(kStageF4 * kThreads * 4 == 64 * kD, "staging split");
-// LDS: two stages of two tiles; after the loop the same bytes carry the
-// partner waves' partial results (4 waves x 32 registers x 64 lanes fp32).
-constexpr int kLdsBytes = 2 * 2 * kTile * 2 > 4 * 32 * 64 * 4 ? 2 * 2 * kTile * 2 : 4 * 32 * 64 * 4;
+// LDS ring of kStages stages, each two fp16 tiles (Q and dO, or K and V) and,
+// for the dK/dV path, the block's two row statistics. After the loop the same
+// bytes carry the partner waves' partial results (4 waves x 32 registers x 64
+// lanes fp32).
+constexpr int kStages = 4;
+constexpr int kStageBytes = 2 * kTile * 2 + 2 * kQBlock * 4;
+constexpr int kRingBytes = kStages * kStageBytes;
+constexpr int kMergeBytes = 4 * 32 * 64 * 4;
+constexpr int kLdsBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
+
+template <int N>
+using Const = std::integral_constant<int, N>;
 
 struct BwdArgs {
   const float *Q, *K, *V, *dO, *LSE, *delta, *blockmax;
@@ -146,14 +157,20 @@ __device__ __forceinline__ void merge_pair(float *buf, int wave, int lane, f32x1
 
 // dK and dV of keys [kv_blk0, kv_blk0 + 128) of one head. Wave w owns keys
 // kv_blk0 + 32*(w%4) .. +31 and query half w/4 of every 64-row block.
-__device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char *lds_raw,
-                          float (*stat)[2][kQBlock]) {
-  half_t(*lds)[2][kTile] = reinterpret_cast<half_t(*)[2][kTile]>(lds_raw);
+//
+// Query block i (rows qb0 = 64*(first_qb + i) ..) goes through ring stage
+// (i - i0) % 4 and staging register set (i - i0) % 2, i0 being the number of
+// blocks that hold the causal diagonal (two, or none without masking): in
+// the unrolled steady loop both are compile-time constants. Block i+3 is
+// written into its stage during iteration i (the stage last read in
+// iteration i-1) and block i+5 is fetched into the register set block i+3
+// has just left.
+__device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char *lds_raw) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, hh = lane >> 5;
   const int kg = wave & 3, qh = wave >> 2;
   const int S = a.S;
-  const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
+  const int ld = a.H * kD, hoff = head * kD;
   const float sigma = head_sigma(a, head, lane);
   const float c2 = a.scale * kLog2e;
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
@@ -177,104 +194,191 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     }
   }
 
-  float4 qreg[kStageF4], doreg[kStageF4];
-  float lreg = 0.f, dreg = 0.f;
-  auto load_block = [&](int qb0) {
+  const int n_qblocks = (S + kQBlock - 1) / kQBlock;
+  const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
+  const int nb = max(n_qblocks - first_qb, 0);
+  // Under causal masking the first two blocks hold the diagonal of the
+  // workgroup's 128 keys; every later row sees every key. i0 is even, so
+  // block i's register set is i % 2.
+  const int i0 = a.causal ? 2 : 0;
+
+  // Per-thread offsets, fixed for the whole loop: rows qh*32 + c of a tile
+  // (A operands of S and dP), this wave's transposed reads (B operands of dV
+  // and dK), the thread's share of the tile stores and its global float4s.
+  int roff[4], troff[2][2][2], soff[kStageF4], goff[kStageF4];
 #pragma unroll
-    for (int i = 0; i < kStageF4; ++i) {
-      // Rows past the end read row S-1 (finite); their lse is +inf, so P = 0.
-      const int idx = tid + i * kThreads;
-      const int row = min(qb0 + (idx >> 4), S - 1), c4 = idx & 15;
-      const size_t off = (size_t)row * ld + hoff + c4 * 4;
-      qreg[i] = *reinterpret_cast<const float4 *>(a.Q + off);
-      doreg[i] = *reinterpret_cast<const float4 *>(a.dO + off);
+  for (int ds = 0; ds < 4; ++ds) roff[ds] = tile_off(qh * 32 + c, 8 * (2 * ds + hh));
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        troff[j][db][hf] = tile_tr4_off(16 * (2 * qh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
+#pragma unroll
+  for (int k = 0; k < kStageF4; ++k) {
+    const int idx = tid + k * kThreads;
+    soff[k] = tile_off(idx >> 4, (idx & 15) * 4);
+    goff[k] = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
+  }
+
+  auto stage_base = [&](int st) { return lds_raw + st * kStageBytes; };
+  // Staged rows of Q and dO (buffer loads on a descriptor based at the
+  // block's first row: rows past S read as zeros) and the block's lse and
+  // Delta (lane = row; every wave loads and stores the same 64 values).
+  float4 qreg[2][kStageF4], greg[2][kStageF4];
+  float lraw[2], draw[2];
+  auto load_block = [&](int i, auto set) {
+    constexpr int b = decltype(set)::value;
+    const int qb0 = (first_qb + i) * kQBlock;
+    const long long rem = (long long)(S - qb0) * ld * 4;
+    const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kQBlock * ld * 4);
+    const size_t base = (size_t)min(qb0, S) * ld;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + base), 0, nrec, kBufferFlags);
+    const auto rg = __builtin_amdgcn_make_buffer_rsrc((void *)(a.dO + base), 0, nrec, kBufferFlags);
+#pragma unroll
+    for (int k = 0; k < kStageF4; ++k) {
+      qreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, goff[k], 0, 0));
+      greg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff[k], 0, 0));
     }
-    if (tid < kQBlock) {
-      const int row = qb0 + tid;
-      const bool ok = row < S;
-      lreg = ok ? a.LSE[(size_t)head * S + row] * kLog2e : INFINITY;
-      dreg = ok ? a.delta[(size_t)head * S + row] : 0.f;
-    }
+    const unsigned srec = (unsigned)max(0, min(S - qb0, kQBlock)) * 4;
+    const size_t sbase = (size_t)head * S + min(qb0, S);
+    const auto rl = __builtin_amdgcn_make_buffer_rsrc((void *)(a.LSE + sbase), 0, srec, kBufferFlags);
+    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void *)(a.delta + sbase), 0, srec, kBufferFlags);
+    lraw[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0));
+    draw[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, lane * 4, 0, 0));
   };
-  auto store_block = [&](int st) {
+  // Q is rounded as c2*Q (the forward's rounding), dO as sigma*dO; the
+  // statistics are stored negated (they enter the products as accumulator
+  // inputs), rows past S get lse = +inf so that P = 0.
+  auto store_block = [&](int i, int st, auto set) {
+    constexpr int b = decltype(set)::value;
+    half_t *qt = reinterpret_cast<half_t *>(stage_base(st));
+    half_t *gt = qt + kTile;
+    float *sl = reinterpret_cast<float *>(gt + kTile);
 #pragma unroll
-    for (int i = 0; i < kStageF4; ++i) {
-      const int idx = tid + i * kThreads;
-      tile_store4(lds[st][0], idx >> 4, (idx & 15) * 4, scale4(qreg[i], c2));
-      tile_store4(lds[st][1], idx >> 4, (idx & 15) * 4, scale4(doreg[i], sigma));
+    for (int k = 0; k < kStageF4; ++k) {
+      *reinterpret_cast<half4_t *>(qt + soff[k]) = to_half4(scale4(qreg[b][k], c2));
+      *reinterpret_cast<half4_t *>(gt + soff[k]) = to_half4(scale4(greg[b][k], sigma));
     }
-    if (tid < kQBlock) {  // negated: they enter the products as accumulator inputs
-      stat[st][0][tid] = -lreg;
-      stat[st][1][tid] = -(dreg * sigma);
-    }
+    const int row = (first_qb + i) * kQBlock + lane;
+    sl[lane] = row < S ? -lraw[b] * kLog2e : -INFINITY;
+    sl[kQBlock + lane] = -(draw[b] * sigma);
   };
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
 
-  const int n_qblocks = (S + kQBlock - 1) / kQBlock;
-  const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
-  if (first_qb < n_qblocks) {
-    load_block(first_qb * kQBlock);
-    store_block(0);
-  }
-  __syncthreads();
-
-  for (int qbi = first_qb; qbi < n_qblocks; ++qbi) {
-    const int st = (qbi - first_qb) & 1;
-    const int qb0 = qbi * kQBlock;
-    const int q0 = qb0 + qh * 32;  // this wave's first query row
-    if (qbi + 1 < n_qblocks) load_block(qb0 + kQBlock);
-    // Rows q0..q0+31 see this wave's keys only if some row >= key0.
-    if (!a.causal || q0 + 31 >= key0) {
-      const half_t *qt = lds[st][0];
-      const half_t *dot = lds[st][1];
-
-      // S - lse2 and dP - Delta: register r is query q0 + 8*(r/4) + 4*hh + r%4
-      // (lane = key); the first MFMA of each chain takes the row's -lse2 /
-      // -Delta as its accumulator input.
-      f32x16 s, dp;
+  // One block. `masked`: the block may hold the causal diagonal, so rows
+  // below this wave's keys are masked and a wave whose rows are all below
+  // its keys skips the block.
+  auto compute = [&](int i, int st, bool masked) {
+    const int q0 = (first_qb + i) * kQBlock + qh * 32;  // this wave's first query row
+    if (masked && q0 + 31 < key0) return;
+    const half_t *qt = reinterpret_cast<const half_t *>(stage_base(st));
+    const half_t *gt = qt + kTile;
+    const float *sl = reinterpret_cast<const float *>(gt + kTile);
+    // S - lse2 and dP - Delta: register r is query q0 + 8*(r/4) + 4*hh + r%4
+    // (lane = key); each chain starts from the rows' -lse2 / -Delta.
+    f32x16 s, dp;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 nl = *reinterpret_cast<const float4 *>(&stat[st][0][qh * 32 + g * 8 + hh * 4]);
-        const float4 nd = *reinterpret_cast<const float4 *>(&stat[st][1][qh * 32 + g * 8 + hh * 4]);
-        s[4 * g] = nl.x; s[4 * g + 1] = nl.y; s[4 * g + 2] = nl.z; s[4 * g + 3] = nl.w;
-        dp[4 * g] = nd.x; dp[4 * g + 1] = nd.y; dp[4 * g + 2] = nd.z; dp[4 * g + 3] = nd.w;
+    for (int g = 0; g < 4; ++g) {
+      const float4 nl = *reinterpret_cast<const float4 *>(sl + qh * 32 + g * 8 + hh * 4);
+      const float4 nd = *reinterpret_cast<const float4 *>(sl + kQBlock + qh * 32 + g * 8 + hh * 4);
+      s[4 * g] = nl.x; s[4 * g + 1] = nl.y; s[4 * g + 2] = nl.z; s[4 * g + 3] = nl.w;
+      dp[4 * g] = nd.x; dp[4 * g + 1] = nd.y; dp[4 * g + 2] = nd.z; dp[4 * g + 3] = nd.w;
+    }
+    half8_t qa[4], ga[4];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      qa[ds] = *reinterpret_cast<const half8_t *>(qt + roff[ds]);
+      ga[ds] = *reinterpret_cast<const half8_t *>(gt + roff[ds]);
+    }
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      s = mfma32x32x16(qa[ds], kf[ds], s);
+      dp = mfma32x32x16(ga[ds], vf[ds], dp);
+    }
+    // dO^T and (c2 Q)^T slots for this wave's two query steps.
+    half8_t gtr[2][2], qtr[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const half4_t g0 = tile_tr4_at(gt, troff[j][db][0]), g1 = tile_tr4_at(gt, troff[j][db][1]);
+        const half4_t q0v = tile_tr4_at(qt, troff[j][db][0]), q1v = tile_tr4_at(qt, troff[j][db][1]);
+        gtr[j][db] = half8_t{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+        qtr[j][db] = half8_t{q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]};
       }
+    // P and dS (dS overwrites dP).
+    if (masked && q0 < key0 + 31) {
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        s = mfma32x32x16(tile_row8(qt, qh * 32 + c, 2 * ds + hh), kf[ds], s);
-        dp = mfma32x32x16(tile_row8(dot, qh * 32 + c, 2 * ds + hh), vf[ds], dp);
-      }
-
-      // P and dS (dS overwrites dP).
-      if (a.causal && q0 < key0 + 31) {
+      for (int r = 0; r < 16; ++r)
+        if (key > q0 + (r >> 2) * 8 + hh * 4 + (r & 3)) s[r] = -INFINITY;
+    }
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (key > q0 + (r >> 2) * 8 + hh * 4 + (r & 3)) s[r] = -INFINITY;
-      }
+    for (int r = 0; r < 16; ++r) {
+      s[r] = fast_exp2(s[r]);
+      dp[r] *= s[r];
+    }
+    // dV += P^T dO, dK += dS^T (c2 Q): A from registers (lane = key).
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = fast_exp2(s[r]);
-        dp[r] *= s[r];
-      }
-
-      // dV += P^T dO, dK += dS^T (c2 Q): A from registers (lane = key), B =
-      // dO^T / Q^T through transposed reads of this wave's 32 rows.
+    for (int j = 0; j < 2; ++j) {
+      const half8_t pf = acc_to_slots(s, j);
+      const half8_t dsf = acc_to_slots(dp, j);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const half8_t pf = acc_to_slots(s, j);
-        const half8_t dsf = acc_to_slots(dp, j);
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          dv[db] = mfma32x32x16(pf, tile_tr8(dot, 2 * qh + j, db, lane), dv[db]);
-          dk[db] = mfma32x32x16(dsf, tile_tr8(qt, 2 * qh + j, db, lane), dk[db]);
-        }
+      for (int db = 0; db < 2; ++db) {
+        dv[db] = mfma32x32x16(pf, gtr[j][db], dv[db]);
+        dk[db] = mfma32x32x16(dsf, qtr[j][db], dk[db]);
       }
     }
-    if (qbi + 1 < n_qblocks) store_block(st ^ 1);
+  };
+
+  // Generic iteration (head and remainder): runtime stage and register set.
+  auto step = [&](int i, bool masked) {
+    compute(i, (i - i0) & 3, masked);
+    if (i + 3 < nb) {
+      if ((i + 3) & 1) {
+        store_block(i + 3, (i + 3 - i0) & 3, Const<1>{});
+        if (i + 5 < nb) load_block(i + 5, Const<1>{});
+      } else {
+        store_block(i + 3, (i + 3 - i0) & 3, Const<0>{});
+        if (i + 5 < nb) load_block(i + 5, Const<0>{});
+      }
+    }
     __syncthreads();
+  };
+
+  // Prologue: blocks 0-2 in the ring, blocks 3 and 4 in registers (loads of
+  // blocks past the end read zeros into stages that are never read).
+  load_block(0, Const<0>{});
+  load_block(1, Const<1>{});
+  store_block(0, (0 - i0) & 3, Const<0>{});
+  load_block(2, Const<0>{});
+  store_block(1, (1 - i0) & 3, Const<1>{});
+  load_block(3, Const<1>{});
+  store_block(2, (2 - i0) & 3, Const<0>{});
+  load_block(4, Const<0>{});
+  __syncthreads();
+
+  int i = 0;
+  for (; i < i0 && i < nb; ++i) step(i, true);
+  // Steady state: no mask, every wave active; stage and set are constants
+  // (i - i0 is a multiple of 4 at the top of each trip).
+  auto iter = [&](int ii, auto u) {
+    constexpr int q = decltype(u)::value;
+    compute(ii, q, false);
+    store_block(ii + 3, (q + 3) & 3, Const<(q + 3) & 1>{});
+    load_block(ii + 5, Const<(q + 3) & 1>{});
+    __syncthreads();
+  };
+  for (; i + 4 <= nb; i += 4) {
+    iter(i, Const<0>{});
+    iter(i + 1, Const<1>{});
+    iter(i + 2, Const<2>{});
+    iter(i + 3, Const<3>{});
   }
+  for (; i < nb; ++i) step(i, false);
 
   float *buf = reinterpret_cast<float *>(lds_raw);
   merge_pair(buf, wave, lane, dk[0], dk[1]);
@@ -302,7 +406,6 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 // dQ of query rows [q_blk0, q_blk0 + 128) of one head. Wave w owns rows
 // q_blk0 + 32*(w%4) .. +31 and key half w/4 of every 64-key tile.
 __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *lds_raw) {
-  half_t(*lds)[2][kTile] = reinterpret_cast<half_t(*)[2][kTile]>(lds_raw);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, hh = lane >> 5;
   const int qg = wave & 3, kh = wave >> 2;
@@ -346,71 +449,146 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 
   const int kv_end = a.causal ? min(S, q_blk0 + kQueriesPerWg) : S;
   const int n_tiles = (kv_end + kKTile - 1) / kKTile;
+  // Tiles below n_full need no mask for any row of the workgroup (causal:
+  // every key is below the first row; otherwise every key is below S). They
+  // run first, unrolled by four; the rest take the general loop.
+  const int n_full = a.causal ? min(q_blk0 / kKTile, n_tiles) : S / kKTile;
 
-  float4 kreg[kStageF4], vreg[kStageF4];
-  auto load_tile = [&](int t) {
-    const int kv0 = t * kKTile;
+  // Per-thread offsets: K/V rows kh*32 + c (A operands of S^T and dP^T), K^T
+  // slots through transposed reads (A operand of dQ^T), tile stores and the
+  // thread's global float4s.
+  int koff[4], ktoff[2][2][2], soff[kStageF4], goff[kStageF4];
 #pragma unroll
-    for (int i = 0; i < kStageF4; ++i) {
-      // Keys past the end read row S-1 (finite) and are masked to P = 0.
-      const int idx = tid + i * kThreads;
-      const int kr = min(kv0 + (idx >> 4), S - 1), c4 = idx & 15;
-      const size_t off = (size_t)kr * ld + hoff + c4 * 4;
-      kreg[i] = *reinterpret_cast<const float4 *>(a.K + off);
-      vreg[i] = *reinterpret_cast<const float4 *>(a.V + off);
+  for (int ds = 0; ds < 4; ++ds) koff[ds] = tile_off(kh * 32 + c, 8 * (2 * ds + hh));
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        ktoff[j][db][hf] = tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
+#pragma unroll
+  for (int k = 0; k < kStageF4; ++k) {
+    const int idx = tid + k * kThreads;
+    soff[k] = tile_off(idx >> 4, (idx & 15) * 4);
+    goff[k] = ((idx >> 4) * (int)ld + (int)hoff + (idx & 15) * 4) * 4;
+  }
+
+  // Tile t goes through ring stage t % 4 and register set t % 2; tile t+3
+  // is written during iteration t (into the stage last read in iteration
+  // t-1) and tile t+5 is fetched into the set tile t+3 has just left. Keys
+  // past S read as zeros and are masked to P = 0.
+  auto stage_base = [&](int st) { return reinterpret_cast<half_t *>(lds_raw + st * kStageBytes); };
+  float4 kreg[2][kStageF4], vreg[2][kStageF4];
+  auto load_tile = [&](int t, auto set) {
+    constexpr int b = decltype(set)::value;
+    const int kv0 = t * kKTile;
+    const long long rem = (long long)(S - kv0) * (long long)ld * 4;
+    const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kKTile * (long long)ld * 4);
+    const size_t base = (size_t)min(kv0, S) * ld;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(a.K + base), 0, nrec, kBufferFlags);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.V + base), 0, nrec, kBufferFlags);
+#pragma unroll
+    for (int k = 0; k < kStageF4; ++k) {
+      kreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, 0));
+      vreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[k], 0, 0));
     }
   };
-  auto store_tile = [&](int st) {
+  auto store_tile = [&](int st, auto set) {
+    constexpr int b = decltype(set)::value;
+    half_t *kt = stage_base(st);
 #pragma unroll
-    for (int i = 0; i < kStageF4; ++i) {
-      const int idx = tid + i * kThreads;
-      tile_store4(lds[st][0], idx >> 4, (idx & 15) * 4, kreg[i]);
-      tile_store4(lds[st][1], idx >> 4, (idx & 15) * 4, vreg[i]);
+    for (int k = 0; k < kStageF4; ++k) {
+      *reinterpret_cast<half4_t *>(kt + soff[k]) = to_half4(kreg[b][k]);
+      *reinterpret_cast<half4_t *>(kt + kTile + soff[k]) = to_half4(vreg[b][k]);
     }
   };
 
   f32x16 dq[2];
   dq[0] = dq[1] = f32x16{};
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+
+  // One tile. `masked`: the tile may hold the causal diagonal or the end of
+  // the keys; a wave that sees none of it skips it.
+  auto compute = [&](int t, int st, bool masked) {
+    const int k0 = t * kKTile + kh * 32;  // first key of this wave's half tile
+    if (masked && !(wave_active && k0 < S && (!a.causal || k0 <= wave_qlast))) return;
+    const half_t *kt = stage_base(st);
+    const half_t *vt = kt + kTile;
+    half8_t ka[4], va[4];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      ka[ds] = *reinterpret_cast<const half8_t *>(kt + koff[ds]);
+      va[ds] = *reinterpret_cast<const half8_t *>(vt + koff[ds]);
+    }
+    // S^T - lse2 and dP^T - Delta: register r is key k0 + 8*(r/4) + 4*hh +
+    // r%4 (lane = query); the chains start from the lane's -lse2 / -Delta.
+    f32x16 s = mfma32x32x16(ka[0], qf[0], negL);
+    f32x16 dp = mfma32x32x16(va[0], gf[0], negD);
+#pragma unroll
+    for (int ds = 1; ds < 4; ++ds) {
+      s = mfma32x32x16(ka[ds], qf[ds], s);
+      dp = mfma32x32x16(va[ds], gf[ds], dp);
+    }
+    half8_t ktr[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const half4_t lo = tile_tr4_at(kt, ktoff[j][db][0]), hi = tile_tr4_at(kt, ktoff[j][db][1]);
+        ktr[j][db] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    if (masked && k0 + 31 > key_lim_lo) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dp[r] *= fast_exp2(s[r]);
+    // dQ^T += K^T dS^T over this wave's two key steps.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const half8_t dsf = acc_to_slots(dp, j);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) dq[db] = mfma32x32x16(ktr[j][db], dsf, dq[db]);
+    }
+  };
+
+  // Prologue: tiles 0-2 in the ring, tiles 3 and 4 in registers.
+  load_tile(0, Const<0>{});
+  load_tile(1, Const<1>{});
+  store_tile(0, Const<0>{});
+  load_tile(2, Const<0>{});
+  store_tile(1, Const<1>{});
+  load_tile(3, Const<1>{});
+  store_tile(2, Const<0>{});
+  load_tile(4, Const<0>{});
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-    const int k0 = t * kKTile + kh * 32;  // first key of this wave's half tile
-    if (wave_active && k0 < S && (!a.causal || k0 <= wave_qlast)) {
-      const half_t *kt = lds[st][0];
-      const half_t *vt = lds[st][1];
-      // S^T - lse2 and dP^T - Delta: register r is key k0 + 8*(r/4) + 4*hh +
-      // r%4 (lane = query); the chains start from the lane's -lse2 / -Delta.
-      f32x16 s = mfma32x32x16(tile_row8(kt, kh * 32 + c, hh), qf[0], negL);
-      f32x16 dp = mfma32x32x16(tile_row8(vt, kh * 32 + c, hh), gf[0], negD);
-#pragma unroll
-      for (int ds = 1; ds < 4; ++ds) {
-        s = mfma32x32x16(tile_row8(kt, kh * 32 + c, 2 * ds + hh), qf[ds], s);
-        dp = mfma32x32x16(tile_row8(vt, kh * 32 + c, 2 * ds + hh), gf[ds], dp);
-      }
-      if (k0 + 31 > key_lim_lo) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] *= fast_exp2(s[r]);
-      // dQ^T += K^T dS^T over this wave's two key steps; K^T through
-      // transposed reads of the K tile.
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const half8_t dsf = acc_to_slots(dp, j);
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-          dq[db] = mfma32x32x16(tile_tr8(kt, 2 * kh + j, db, lane), dsf, dq[db]);
+  auto iter = [&](int t, auto u) {
+    constexpr int q = decltype(u)::value;
+    compute(t, q, false);
+    store_tile((q + 3) & 3, Const<(q + 3) & 1>{});
+    load_tile(t + 5, Const<(q + 3) & 1>{});
+    __syncthreads();
+  };
+  int t = 0;
+  for (; t + 4 <= n_full; t += 4) {
+    iter(t, Const<0>{});
+    iter(t + 1, Const<1>{});
+    iter(t + 2, Const<2>{});
+    iter(t + 3, Const<3>{});
+  }
+  for (; t < n_tiles; ++t) {
+    compute(t, t & 3, true);
+    if (t + 3 < n_tiles) {
+      if ((t + 3) & 1) {
+        store_tile((t + 3) & 3, Const<1>{});
+        if (t + 5 < n_tiles) load_tile(t + 5, Const<1>{});
+      } else {
+        store_tile((t + 3) & 3, Const<0>{});
+        if (t + 5 < n_tiles) load_tile(t + 5, Const<0>{});
       }
     }
-    if (t + 1 < n_tiles) store_tile(st ^ 1);
     __syncthreads();
   }
 
@@ -433,18 +611,26 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 
 // Workgroup b: the two item lists (dK/dV key tiles, dQ query tiles), each
 // ordered longest first under causal masking and round robin over heads,
-// alternate while both last; the longer list's remainder follows.
+// alternate while both last; the longer list's remainder follows. The
+// dispatcher deals workgroup b to XCD b % 8, so the alternation runs within
+// each XCD's share (b / 8) rather than over b: alternating on b itself would
+// put every dK/dV item on the even XCDs and every dQ item on the odd ones.
 __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, int n_kv_items,
                                                              int n_q_items) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
-  __shared__ __attribute__((aligned(16))) float stat[2][2][kQBlock];
   const int b = blockIdx.x;
   const int pairs = min(n_kv_items, n_q_items);
+  const int spread = (2 * pairs) & ~15;  // blocks dealt evenly over the 8 XCDs
   bool kv_item;
   int item;
-  if (b < 2 * pairs) {
-    kv_item = (b & 1) == 0;
-    item = b >> 1;
+  if (b < spread) {
+    const int i = b >> 3;
+    kv_item = (i & 1) == 0;
+    item = (i >> 1) * 8 + (b & 7);
+  } else if (b < 2 * pairs) {
+    const int r = b - spread;
+    kv_item = (r & 1) == 0;
+    item = spread / 2 + (r >> 1);
   } else {
     kv_item = n_kv_items > n_q_items;
     item = b - pairs;
@@ -452,7 +638,7 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, int n_kv_
   const int head = item % a.H;
   const int rank = item / a.H;
   if (kv_item) {
-    dkdv_path(a, head, rank * kKeysPerWg, lds_raw, stat);  // key tile 0 sees the most queries
+    dkdv_path(a, head, rank * kKeysPerWg, lds_raw);  // key tile 0 sees the most queries
   } else {
     const int n_qtiles = n_q_items / a.H;
     const int qtile = a.causal ? n_qtiles - 1 - rank : rank;
