@@ -117,6 +117,11 @@ constexpr int kLdsBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
 template <int N>
 using Const = std::integral_constant<int, N>;
 
+// Relative cost of one step of each item kind (measured at C2: a dK/dV step,
+// four products over a 64-row block, takes about 1.3 times a dQ step).
+constexpr int kCostKvStep = 32;
+constexpr int kCostQStep = 25;
+
 struct BwdArgs {
   const float *Q, *K, *V, *dO, *LSE, *delta, *blockmax;
   float *dQ, *dK, *dV;
@@ -609,39 +614,57 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   }
 }
 
-// Workgroup b: the two item lists (dK/dV key tiles, dQ query tiles), each
-// ordered longest first under causal masking and round robin over heads,
-// alternate while both last; the longer list's remainder follows. The
-// dispatcher deals workgroup b to XCD b % 8, so the alternation runs within
-// each XCD's share (b / 8) rather than over b: alternating on b itself would
-// put every dK/dV item on the even XCDs and every dQ item on the odd ones.
-__global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, int n_kv_items,
-                                                             int n_q_items) {
+// Dispatch order. A dK/dV item of key rank i (keys 128*i ..) walks
+// steps_kv(i) query blocks, a dQ item of query rank j (the j-th longest
+// query tile) steps_q(j) key tiles; their costs are w_kv and w_q per step
+// (a dK/dV step runs four products, a dQ step three). Workgroup b takes the
+// b-th item of both lists merged by decreasing cost (each rank contributes
+// one item per head), so the greedy dispatcher approximates a
+// longest-processing-time schedule, and consecutive items, which the
+// dispatcher deals to different XCDs, mix both kinds.
+struct Sched {
+  int n_qblocks, n_qtiles, S, causal, w_kv, w_q, r_kv, r_q;
+  __device__ int cost_kv(int i) const {
+    const int first_qb = causal ? i * (kKeysPerWg / kQBlock) : 0;
+    return w_kv * max(n_qblocks - first_qb, 0);
+  }
+  __device__ int cost_q(int j) const {
+    const int qtile = causal ? n_qtiles - 1 - j : j;
+    const int kv_end = causal ? min(S, (qtile + 1) * kQueriesPerWg) : S;
+    return w_q * ((kv_end + kKTile - 1) / kKTile);
+  }
+  // Number of query ranks costlier than x (cost_q does not increase with j).
+  __device__ int q_above(int x) const {
+    int lo = 0, hi = r_q;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (cost_q(mid) > x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+  }
+  // Rank k of the merged list (ties: dK/dV first) -> (is dK/dV, rank).
+  __device__ void pick(int k, bool &kv, int &rank) const {
+    int lo = 0, hi = r_kv;  // count of dK/dV ranks merged before position k
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (mid + q_above(cost_kv(mid)) < k) lo = mid + 1; else hi = mid;
+    }
+    kv = lo < r_kv && lo + q_above(cost_kv(lo)) == k;
+    rank = kv ? lo : k - lo;
+  }
+};
+
+__global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sched) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
   const int b = blockIdx.x;
-  const int pairs = min(n_kv_items, n_q_items);
-  const int spread = (2 * pairs) & ~15;  // blocks dealt evenly over the 8 XCDs
   bool kv_item;
-  int item;
-  if (b < spread) {
-    const int i = b >> 3;
-    kv_item = (i & 1) == 0;
-    item = (i >> 1) * 8 + (b & 7);
-  } else if (b < 2 * pairs) {
-    const int r = b - spread;
-    kv_item = (r & 1) == 0;
-    item = spread / 2 + (r >> 1);
-  } else {
-    kv_item = n_kv_items > n_q_items;
-    item = b - pairs;
-  }
-  const int head = item % a.H;
-  const int rank = item / a.H;
+  int rank;
+  sched.pick(b / a.H, kv_item, rank);
+  const int head = b % a.H;
   if (kv_item) {
-    dkdv_path(a, head, rank * kKeysPerWg, lds_raw);  // key tile 0 sees the most queries
+    dkdv_path(a, head, rank * kKeysPerWg, lds_raw);
   } else {
-    const int n_qtiles = n_q_items / a.H;
-    const int qtile = a.causal ? n_qtiles - 1 - rank : rank;
+    const int qtile = a.causal ? sched.n_qtiles - 1 - rank : rank;
     dq_path(a, head, qtile * kQueriesPerWg, lds_raw);
   }
 }
@@ -682,10 +705,17 @@ hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, c
   a.causal = causal ? 1 : 0;
   a.n_pre_blocks = pre_blocks(seq_len);
   a.scale = scale;
-  const int n_kv_items = n_heads * ((seq_len + kKeysPerWg - 1) / kKeysPerWg);
-  const int n_q_items = n_heads * ((seq_len + kQueriesPerWg - 1) / kQueriesPerWg);
-  hipLaunchKernelGGL(bwd_main_kernel, dim3((unsigned)(n_kv_items + n_q_items)), dim3(kThreads), 0,
-                     stream, a, n_kv_items, n_q_items);
+  Sched sched;
+  sched.n_qblocks = (seq_len + kQBlock - 1) / kQBlock;
+  sched.n_qtiles = (seq_len + kQueriesPerWg - 1) / kQueriesPerWg;
+  sched.S = seq_len;
+  sched.causal = causal ? 1 : 0;
+  sched.w_kv = kCostKvStep;
+  sched.w_q = kCostQStep;
+  sched.r_kv = (seq_len + kKeysPerWg - 1) / kKeysPerWg;
+  sched.r_q = sched.n_qtiles;
+  const unsigned n_items = (unsigned)(n_heads * (sched.r_kv + sched.r_q));
+  hipLaunchKernelGGL(bwd_main_kernel, dim3(n_items), dim3(kThreads), 0, stream, a, sched);
   return hipGetLastError();
 }
 
