@@ -112,7 +112,13 @@ constexpr int kStages = 4;
 constexpr int kStageBytes = 2 * kTile * 2 + 2 * kQBlock * 4;
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kMergeBytes = 4 * 32 * 64 * 4;
-constexpr int kLdsBytes = kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes;
+// After the ring: the workgroup's own 128 rows of K and V (dK/dV path) or of
+// c2*Q and sigma*dO (dQ path) as two [128][64] fp16 tiles, staged once with
+// coalesced loads; each wave reads its register fragments from there.
+constexpr int kOwnTile = 128 * kD;  // halves
+constexpr int kOwnBytes = 2 * kOwnTile * 2;
+constexpr int kOwnF4 = 128 * kD / 4 / kThreads;  // float4 per thread per own tile
+constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes;
 
 template <int N>
 using Const = std::integral_constant<int, N>;
@@ -130,12 +136,16 @@ struct BwdArgs {
 };
 
 // Per-head sigma (power of two) from the preprocess block maxima of |dO|.
-__device__ __forceinline__ float head_sigma(const BwdArgs &a, int head, int lane) {
+// Split in two so that a workgroup's prologue can issue every global load it
+// needs before waiting on any: head_blockmax loads (the lane's share of the
+// block maxima), head_sigma reduces.
+__device__ __forceinline__ float head_blockmax(const BwdArgs &a, int head, int lane) {
   float gmax = 0.f;
   for (int i = lane; i < a.n_pre_blocks; i += 64)
     gmax = fmaxf(gmax, a.blockmax[(size_t)head * a.n_pre_blocks + i]);
-  return pow2_scale(wave_max(gmax));
+  return gmax;
 }
+__device__ __forceinline__ float head_sigma(float lane_max) { return pow2_scale(wave_max(lane_max)); }
 
 // Partner waves (w, w+4) hold partial sums of the same 32x32 accumulator
 // blocks: wave w+4 hands its two blocks to wave w through LDS (after a
@@ -176,26 +186,28 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int kg = wave & 3, qh = wave >> 2;
   const int S = a.S;
   const int ld = a.H * kD, hoff = head * kD;
-  const float sigma = head_sigma(a, head, lane);
+  const float bmax = head_blockmax(a, head, lane);
   const float c2 = a.scale * kLog2e;
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
   const int key = key0 + c;
-  const bool key_ok = key < S;
 
   // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
   // holds its key, slots d = 16*ds + 8*hh + j.
+  // (Read from the workgroup's K/V tiles after the prologue; the rows of keys
+  // kv_blk0 .. +127 are fetched with coalesced buffer loads first.)
   half8_t kf[4], vf[4];
+  float4 kown[kOwnF4], vown[kOwnF4];
   {
-    const float *kp = a.K + (key_ok ? (size_t)key * ld + hoff : 0);
-    const float *vp = a.V + (key_ok ? (size_t)key * ld + hoff : 0);
+    const unsigned rows = (unsigned)max(0, min(S - kv_blk0, 128));
+    const size_t base = (size_t)min(kv_blk0, S) * ld;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(a.K + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.V + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const half4_t k0 = to_half4(load4_or_zero(kp + ds * 16 + hh * 8, key_ok));
-      const half4_t k1 = to_half4(load4_or_zero(kp + ds * 16 + hh * 8 + 4, key_ok));
-      const half4_t v0 = to_half4(load4_or_zero(vp + ds * 16 + hh * 8, key_ok));
-      const half4_t v1 = to_half4(load4_or_zero(vp + ds * 16 + hh * 8 + 4, key_ok));
-      kf[ds] = half8_t{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
-      vf[ds] = half8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    for (int k = 0; k < kOwnF4; ++k) {
+      const int idx = tid + k * kThreads;
+      const int off = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
+      kown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      vown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
     }
   }
 
@@ -233,8 +245,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // Delta (lane = row; every wave loads and stores the same 64 values).
   float4 qreg[2][kStageF4], greg[2][kStageF4];
   float lraw[2], draw[2];
-  auto load_block = [&](int i, auto set) {
-    constexpr int b = decltype(set)::value;
+  auto load_regs = [&](int i, float4 (&qr)[kStageF4], float4 (&gr)[kStageF4], float &lr, float &dr) {
     const int qb0 = (first_qb + i) * kQBlock;
     const long long rem = (long long)(S - qb0) * ld * 4;
     const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kQBlock * ld * 4);
@@ -243,32 +254,41 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     const auto rg = __builtin_amdgcn_make_buffer_rsrc((void *)(a.dO + base), 0, nrec, kBufferFlags);
 #pragma unroll
     for (int k = 0; k < kStageF4; ++k) {
-      qreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, goff[k], 0, 0));
-      greg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff[k], 0, 0));
+      qr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, goff[k], 0, 0));
+      gr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff[k], 0, 0));
     }
     const unsigned srec = (unsigned)max(0, min(S - qb0, kQBlock)) * 4;
     const size_t sbase = (size_t)head * S + min(qb0, S);
     const auto rl = __builtin_amdgcn_make_buffer_rsrc((void *)(a.LSE + sbase), 0, srec, kBufferFlags);
     const auto rd = __builtin_amdgcn_make_buffer_rsrc((void *)(a.delta + sbase), 0, srec, kBufferFlags);
-    lraw[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0));
-    draw[b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, lane * 4, 0, 0));
+    lr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0));
+    dr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, lane * 4, 0, 0));
   };
   // Q is rounded as c2*Q (the forward's rounding), dO as sigma*dO; the
   // statistics are stored negated (they enter the products as accumulator
   // inputs), rows past S get lse = +inf so that P = 0.
-  auto store_block = [&](int i, int st, auto set) {
-    constexpr int b = decltype(set)::value;
+  float sigma = 1.f;
+  auto store_regs = [&](int i, int st, const float4 (&qr)[kStageF4], const float4 (&gr)[kStageF4], float lr,
+                        float dr) {
     half_t *qt = reinterpret_cast<half_t *>(stage_base(st));
     half_t *gt = qt + kTile;
     float *sl = reinterpret_cast<float *>(gt + kTile);
 #pragma unroll
     for (int k = 0; k < kStageF4; ++k) {
-      *reinterpret_cast<half4_t *>(qt + soff[k]) = to_half4(scale4(qreg[b][k], c2));
-      *reinterpret_cast<half4_t *>(gt + soff[k]) = to_half4(scale4(greg[b][k], sigma));
+      *reinterpret_cast<half4_t *>(qt + soff[k]) = round_scaled4(qr[k], c2);
+      *reinterpret_cast<half4_t *>(gt + soff[k]) = to_half4(scale4(gr[k], sigma));
     }
     const int row = (first_qb + i) * kQBlock + lane;
-    sl[lane] = row < S ? -lraw[b] * kLog2e : -INFINITY;
-    sl[kQBlock + lane] = -(draw[b] * sigma);
+    sl[lane] = row < S ? -lr * kLog2e : -INFINITY;
+    sl[kQBlock + lane] = -(dr * sigma);
+  };
+  auto load_block = [&](int i, auto set) {
+    constexpr int b = decltype(set)::value;
+    load_regs(i, qreg[b], greg[b], lraw[b], draw[b]);
+  };
+  auto store_block = [&](int i, int st, auto set) {
+    constexpr int b = decltype(set)::value;
+    store_regs(i, st, qreg[b], greg[b], lraw[b], draw[b]);
   };
 
   f32x16 dk[2], dv[2];
@@ -354,17 +374,39 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     __syncthreads();
   };
 
-  // Prologue: blocks 0-2 in the ring, blocks 3 and 4 in registers (loads of
-  // blocks past the end read zeros into stages that are never read).
-  load_block(0, Const<0>{});
-  load_block(1, Const<1>{});
-  store_block(0, (0 - i0) & 3, Const<0>{});
-  load_block(2, Const<0>{});
-  store_block(1, (1 - i0) & 3, Const<1>{});
-  load_block(3, Const<1>{});
-  store_block(2, (2 - i0) & 3, Const<0>{});
-  load_block(4, Const<0>{});
+  // Prologue: every load is issued before the first wait (blocks 0-2 into
+  // prologue registers, blocks 3 and 4 into their sets; loads past the end
+  // read zeros into stages that are never read), then sigma, then blocks 0-2
+  // go into the ring.
+  {
+    float4 qp[3][kStageF4], gp[3][kStageF4];
+    float lp[3], dpr[3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) load_regs(p, qp[p], gp[p], lp[p], dpr[p]);
+    load_block(3, Const<1>{});
+    load_block(4, Const<0>{});
+    sigma = head_sigma(bmax);
+    half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+#pragma unroll
+    for (int k = 0; k < kOwnF4; ++k) {
+      const int idx = tid + k * kThreads;
+      *reinterpret_cast<half4_t *>(own + tile_off(idx >> 4, (idx & 15) * 4)) = to_half4(kown[k]);
+      *reinterpret_cast<half4_t *>(own + kOwnTile + tile_off(idx >> 4, (idx & 15) * 4)) = to_half4(vown[k]);
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) store_regs(p, (p - i0) & 3, qp[p], gp[p], lp[p], dpr[p]);
+  }
   __syncthreads();
+  {
+    // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
+    // holds key key0 + c, slots d = 16*ds + 8*hh + j.
+    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      kf[ds] = *reinterpret_cast<const half8_t *>(own + tile_off(kg * 32 + c, 8 * (2 * ds + hh)));
+      vf[ds] = *reinterpret_cast<const half8_t *>(own + kOwnTile + tile_off(kg * 32 + c, 8 * (2 * ds + hh)));
+    }
+  }
 
   int i = 0;
   for (; i < i0 && i < nb; ++i) step(i, true);
@@ -416,7 +458,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int qg = wave & 3, kh = wave >> 2;
   const int S = a.S;
   const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
-  const float sigma = head_sigma(a, head, lane);
+  const float bmax = head_blockmax(a, head, lane);
   const float c2 = a.scale * kLog2e;
   const int q_w0 = q_blk0 + qg * 32;
   const int query = q_w0 + c;
@@ -428,29 +470,28 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int key_lim = a.causal ? min(query, S - 1) : S - 1;
   const int key_lim_lo = a.causal ? min(q_w0, S - 1) : S - 1;
 
-  // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds its query.
-  half8_t qf[4], gf[4];
+  // Raw Q / dO rows and row statistics of the lane's query; they become the
+  // (c2 Q)^T and (sigma dO)^T fragments (B operands, lane c holds its query)
+  // once sigma is known, after the prologue has issued every load.
+  float4 qown[kOwnF4], gown[kOwnF4];
   {
-    const float *qp = a.Q + (q_ok ? (size_t)query * ld + hoff : 0);
-    const float *gp = a.dO + (q_ok ? (size_t)query * ld + hoff : 0);
+    const unsigned rows = (unsigned)max(0, min(S - q_blk0, 128));
+    const size_t base = (size_t)min(q_blk0, S) * ld;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
+    const auto rg = __builtin_amdgcn_make_buffer_rsrc((void *)(a.dO + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const half4_t q0 = to_half4(scale4(load4_or_zero(qp + ds * 16 + hh * 8, q_ok), c2));
-      const half4_t q1 = to_half4(scale4(load4_or_zero(qp + ds * 16 + hh * 8 + 4, q_ok), c2));
-      const half4_t g0 = to_half4(scale4(load4_or_zero(gp + ds * 16 + hh * 8, q_ok), sigma));
-      const half4_t g1 = to_half4(scale4(load4_or_zero(gp + ds * 16 + hh * 8 + 4, q_ok), sigma));
-      qf[ds] = half8_t{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
-      gf[ds] = half8_t{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    for (int k = 0; k < kOwnF4; ++k) {
+      const int idx = tid + k * kThreads;
+      const int off = (int)(((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4);
+      qown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
+      gown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
     }
   }
-  const float L = q_ok ? a.LSE[(size_t)head * S + query] * kLog2e : INFINITY;
-  const float Dl = q_ok ? a.delta[(size_t)head * S + query] * sigma : 0.f;
+  const float Lraw = q_ok ? a.LSE[(size_t)head * S + query] : 0.f;
+  const float Draw = q_ok ? a.delta[(size_t)head * S + query] : 0.f;
+  half8_t qf[4], gf[4];
   f32x16 negL, negD;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    negL[r] = -L;
-    negD[r] = -Dl;
-  }
+  float sigma;
 
   const int kv_end = a.causal ? min(S, q_blk0 + kQueriesPerWg) : S;
   const int n_tiles = (kv_end + kKTile - 1) / kKTile;
@@ -485,8 +526,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // past S read as zeros and are masked to P = 0.
   auto stage_base = [&](int st) { return reinterpret_cast<half_t *>(lds_raw + st * kStageBytes); };
   float4 kreg[2][kStageF4], vreg[2][kStageF4];
-  auto load_tile = [&](int t, auto set) {
-    constexpr int b = decltype(set)::value;
+  auto load_regs = [&](int t, float4 (&kr)[kStageF4], float4 (&vr)[kStageF4]) {
     const int kv0 = t * kKTile;
     const long long rem = (long long)(S - kv0) * (long long)ld * 4;
     const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kKTile * (long long)ld * 4);
@@ -495,18 +535,25 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.V + base), 0, nrec, kBufferFlags);
 #pragma unroll
     for (int k = 0; k < kStageF4; ++k) {
-      kreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, 0));
-      vreg[b][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[k], 0, 0));
+      kr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, 0));
+      vr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[k], 0, 0));
     }
   };
-  auto store_tile = [&](int st, auto set) {
-    constexpr int b = decltype(set)::value;
+  auto store_regs = [&](int st, const float4 (&kr)[kStageF4], const float4 (&vr)[kStageF4]) {
     half_t *kt = stage_base(st);
 #pragma unroll
     for (int k = 0; k < kStageF4; ++k) {
-      *reinterpret_cast<half4_t *>(kt + soff[k]) = to_half4(kreg[b][k]);
-      *reinterpret_cast<half4_t *>(kt + kTile + soff[k]) = to_half4(vreg[b][k]);
+      *reinterpret_cast<half4_t *>(kt + soff[k]) = to_half4(kr[k]);
+      *reinterpret_cast<half4_t *>(kt + kTile + soff[k]) = to_half4(vr[k]);
     }
+  };
+  auto load_tile = [&](int t, auto set) {
+    constexpr int b = decltype(set)::value;
+    load_regs(t, kreg[b], vreg[b]);
+  };
+  auto store_tile = [&](int st, auto set) {
+    constexpr int b = decltype(set)::value;
+    store_regs(st, kreg[b], vreg[b]);
   };
 
   f32x16 dq[2];
@@ -558,16 +605,45 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     }
   };
 
-  // Prologue: tiles 0-2 in the ring, tiles 3 and 4 in registers.
-  load_tile(0, Const<0>{});
-  load_tile(1, Const<1>{});
-  store_tile(0, Const<0>{});
-  load_tile(2, Const<0>{});
-  store_tile(1, Const<1>{});
-  load_tile(3, Const<1>{});
-  store_tile(2, Const<0>{});
-  load_tile(4, Const<0>{});
+  // Prologue: every load is issued before the first wait (tiles 0-2 into
+  // prologue registers, tiles 3 and 4 into their sets), then sigma and the
+  // fragments, then tiles 0-2 go into the ring.
+  {
+    float4 kp[3][kStageF4], vp[3][kStageF4];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
+    load_tile(3, Const<1>{});
+    load_tile(4, Const<0>{});
+    sigma = head_sigma(bmax);
+    half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+#pragma unroll
+    for (int k = 0; k < kOwnF4; ++k) {
+      const int idx = tid + k * kThreads;
+      *reinterpret_cast<half4_t *>(own + tile_off(idx >> 4, (idx & 15) * 4)) = round_scaled4(qown[k], c2);
+      *reinterpret_cast<half4_t *>(own + kOwnTile + tile_off(idx >> 4, (idx & 15) * 4)) =
+          to_half4(scale4(gown[k], sigma));
+    }
+    const float L = q_ok ? Lraw * kLog2e : INFINITY;
+    const float Dl = Draw * sigma;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      negL[r] = -L;
+      negD[r] = -Dl;
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) store_regs(p & 3, kp[p], vp[p]);
+  }
   __syncthreads();
+  {
+    // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds query
+    // q_w0 + c, slots d = 16*ds + 8*hh + j.
+    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      qf[ds] = *reinterpret_cast<const half8_t *>(own + tile_off(qg * 32 + c, 8 * (2 * ds + hh)));
+      gf[ds] = *reinterpret_cast<const half8_t *>(own + kOwnTile + tile_off(qg * 32 + c, 8 * (2 * ds + hh)));
+    }
+  }
 
   auto iter = [&](int t, auto u) {
     constexpr int q = decltype(u)::value;
@@ -622,19 +698,22 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 // one item per head), so the greedy dispatcher approximates a
 // longest-processing-time schedule, and consecutive items, which the
 // dispatcher deals to different XCDs, mix both kinds.
+constexpr int kSchedTable = 512;  // merged ranks listed in the kernel arguments when they fit
 struct Sched {
   int n_qblocks, n_qtiles, S, causal, w_kv, w_q, r_kv, r_q;
-  __device__ int cost_kv(int i) const {
+  int use_table;
+  unsigned short table[kSchedTable];  // (is dK/dV) << 15 | rank, in merged order
+  __host__ __device__ int cost_kv(int i) const {
     const int first_qb = causal ? i * (kKeysPerWg / kQBlock) : 0;
     return w_kv * max(n_qblocks - first_qb, 0);
   }
-  __device__ int cost_q(int j) const {
+  __host__ __device__ int cost_q(int j) const {
     const int qtile = causal ? n_qtiles - 1 - j : j;
     const int kv_end = causal ? min(S, (qtile + 1) * kQueriesPerWg) : S;
     return w_q * ((kv_end + kKTile - 1) / kKTile);
   }
   // Number of query ranks costlier than x (cost_q does not increase with j).
-  __device__ int q_above(int x) const {
+  __host__ __device__ int q_above(int x) const {
     int lo = 0, hi = r_q;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -643,7 +722,7 @@ struct Sched {
     return lo;
   }
   // Rank k of the merged list (ties: dK/dV first) -> (is dK/dV, rank).
-  __device__ void pick(int k, bool &kv, int &rank) const {
+  __host__ __device__ void pick(int k, bool &kv, int &rank) const {
     int lo = 0, hi = r_kv;  // count of dK/dV ranks merged before position k
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -659,7 +738,13 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
   const int b = blockIdx.x;
   bool kv_item;
   int rank;
-  sched.pick(b / a.H, kv_item, rank);
+  if (sched.use_table) {
+    const unsigned t = sched.table[b / a.H];
+    kv_item = (t >> 15) != 0;
+    rank = (int)(t & 0x7fff);
+  } else {
+    sched.pick(b / a.H, kv_item, rank);
+  }
   const int head = b % a.H;
   if (kv_item) {
     dkdv_path(a, head, rank * kKeysPerWg, lds_raw);
@@ -714,6 +799,15 @@ hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, c
   sched.w_q = kCostQStep;
   sched.r_kv = (seq_len + kKeysPerWg - 1) / kKeysPerWg;
   sched.r_q = sched.n_qtiles;
+  // The merged order, computed here once when it fits in the arguments (the
+  // in-kernel search costs each workgroup about 2 us).
+  sched.use_table = sched.r_kv + sched.r_q <= kSchedTable ? 1 : 0;
+  for (int k = 0; k < kSchedTable; ++k) {
+    bool kv = false;
+    int rank = 0;
+    if (sched.use_table && k < sched.r_kv + sched.r_q) sched.pick(k, kv, rank);
+    sched.table[k] = (unsigned short)((kv ? 0x8000u : 0u) | (unsigned)rank);
+  }
   const unsigned n_items = (unsigned)(n_heads * (sched.r_kv + sched.r_q));
   hipLaunchKernelGGL(bwd_main_kernel, dim3(n_items), dim3(kThreads), 0, stream, a, sched);
   return hipGetLastError();

@@ -87,15 +87,16 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   const int n_main = min(n_full, n_tiles - 1);
 
   // Q^T fragments (B operand): lane c holds its query, slots d = 16*ds + 8*hh + j.
+  // (Loaded raw here; converted after the prologue has issued every load.)
   half8_t qf[4];
+  float4 qraw[8];
   {
     const bool ok = query < S;
     const float *p = Q + (ok ? (size_t)query * ld + hoff : 0);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
-      const half4_t lo = to_half4(scale4(load4_or_zero(p + ds * 16 + hh * 8, ok), qscale));
-      const half4_t hi = to_half4(scale4(load4_or_zero(p + ds * 16 + hh * 8 + 4, ok), qscale));
-      qf[ds] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      qraw[2 * ds] = load4_or_zero(p + ds * 16 + hh * 8, ok);
+      qraw[2 * ds + 1] = load4_or_zero(p + ds * 16 + hh * 8 + 4, ok);
     }
   }
 
@@ -125,8 +126,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   // Two register sets of staged K/V float4s (set t % 2 holds tile t), so a
   // tile is fetched two iterations before it is written to LDS.
   float4 kreg[2][kF4], vreg[2][kF4];
-  auto load_tile = [&](int t, auto set) {
-    constexpr int b = decltype(set)::value;
+  auto load_regs = [&](int t, float4 (&kr)[kF4], float4 (&vr)[kF4]) {
     const int kv0 = t * kBN;
     const long long rem = (long long)(S - kv0) * ld * 4;
     const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kBN * ld * 4);
@@ -135,18 +135,25 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(V + base), 0, nrec, kBufferFlags);
 #pragma unroll
     for (int i = 0; i < kF4; ++i) {
-      kreg[b][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[i], 0, 0));
-      vreg[b][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[i], 0, 0));
+      kr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[i], 0, 0));
+      vr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[i], 0, 0));
     }
   };
-  auto store_tile = [&](int stage, auto set) {
-    constexpr int b = decltype(set)::value;
+  auto store_regs = [&](int stage, const float4 (&kr)[kF4], const float4 (&vr)[kF4]) {
     half_t *kt = ring + stage * kStageHalves;
 #pragma unroll
     for (int i = 0; i < kF4; ++i) {
-      *reinterpret_cast<half4_t *>(kt + soff[i]) = to_half4(kreg[b][i]);
-      *reinterpret_cast<half4_t *>(kt + kTile + soff[i]) = to_half4(vreg[b][i]);
+      *reinterpret_cast<half4_t *>(kt + soff[i]) = to_half4(kr[i]);
+      *reinterpret_cast<half4_t *>(kt + kTile + soff[i]) = to_half4(vr[i]);
     }
+  };
+  auto load_tile = [&](int t, auto set) {
+    constexpr int b = decltype(set)::value;
+    load_regs(t, kreg[b], vreg[b]);
+  };
+  auto store_tile = [&](int stage, auto set) {
+    constexpr int b = decltype(set)::value;
+    store_regs(stage, kreg[b], vreg[b]);
   };
   using Set0 = std::integral_constant<int, 0>;
   using Set1 = std::integral_constant<int, 1>;
@@ -227,15 +234,24 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       for (int db = 0; db < 2; ++db) o[db] = mfma32x32x16(vf[j][db], pf[j], o[db]);
   };
 
-  // Prologue: tiles 0-2 in the ring, tiles 3 and 4 in registers, S of tile 0.
-  load_tile(0, Set0{});
-  load_tile(1, Set1{});
-  store_tile(0, Set0{});
-  load_tile(2, Set0{});
-  store_tile(1, Set1{});
-  load_tile(3, Set1{});
-  store_tile(2, Set0{});
-  load_tile(4, Set0{});
+  // Prologue: every load is issued before the first wait (Q above, tiles 0-2
+  // into prologue registers, tiles 3 and 4 into their sets), then tiles 0-2
+  // go into the ring and S of tile 0 is computed.
+  {
+    float4 kp[3][kF4], vp[3][kF4];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
+    load_tile(3, Set1{});
+    load_tile(4, Set0{});
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const half4_t lo = round_scaled4(qraw[2 * ds], qscale);
+      const half4_t hi = round_scaled4(qraw[2 * ds + 1], qscale);
+      qf[ds] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) store_regs(p, kp[p], vp[p]);
+  }
   __syncthreads();
   f32x16 s;
   {

@@ -51,6 +51,17 @@ __device__ __forceinline__ float4 scale4(float4 v, float s) {
   return make_float4(v.x * s, v.y * s, v.z * s, v.w * s);
 }
 
+// fp16(fp32(v * s)): the product is rounded to fp32 first, then to fp16. The
+// forward and both backward paths round c2 * Q through this one function, so
+// the backward recomputes exactly the forward's scores; the empty asm keeps
+// the compiler from fusing the product into a single-rounding mixed-precision
+// FMA in some call sites and not in others.
+__device__ __forceinline__ half4_t round_scaled4(float4 v, float s) {
+  float4 p = scale4(v, s);
+  asm volatile("" : "+v"(p.x), "+v"(p.y), "+v"(p.z), "+v"(p.w));
+  return to_half4(p);
+}
+
 __device__ __forceinline__ float4 load4_or_zero(const float *p, bool ok) {
   return ok ? *reinterpret_cast<const float4 *>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
