@@ -47,7 +47,11 @@ constexpr int kMergeRegs = 34;
 constexpr float kRescale = 8.f;  // log2 headroom of the softmax reference point
 constexpr int kRingBytes = kStages * kStageHalves * 2;
 constexpr int kMergeBytes = 4 * kMergeRegs * 64 * 4;
-constexpr int kLdsBytes = kMergeBytes > kRingBytes ? kMergeBytes : kRingBytes;
+// After the ring: the workgroup's 128 Q rows as a [128][64] fp16 tile (c2 Q),
+// staged once with coalesced loads; each wave reads its fragments from it.
+constexpr int kQTileBytes = kBM * kD * 2;
+constexpr int kQF4 = kBM * kD / 4 / kThreads;  // float4 of Q per thread
+constexpr int kLdsBytes = (kMergeBytes > kRingBytes ? kMergeBytes : kRingBytes) + kQTileBytes;
 
 template <int N>
 using Stage = std::integral_constant<int, N>;
@@ -86,17 +90,19 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   const int n_full = causal ? min(q_blk0 / kBN, n_tiles) : S / kBN;
   const int n_main = min(n_full, n_tiles - 1);
 
-  // Q^T fragments (B operand): lane c holds its query, slots d = 16*ds + 8*hh + j.
-  // (Loaded raw here; converted after the prologue has issued every load.)
+  // The workgroup's Q rows arrive here by coalesced buffer loads; they are
+  // rounded into LDS after the prologue has issued every load, and each wave
+  // then reads its Q^T fragments from there.
   half8_t qf[4];
-  float4 qraw[8];
+  float4 qraw[kQF4];
   {
-    const bool ok = query < S;
-    const float *p = Q + (ok ? (size_t)query * ld + hoff : 0);
+    const unsigned rows = (unsigned)max(0, min(S - q_blk0, kBM));
+    const size_t base = (size_t)min(q_blk0, S) * ld;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(Q + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      qraw[2 * ds] = load4_or_zero(p + ds * 16 + hh * 8, ok);
-      qraw[2 * ds + 1] = load4_or_zero(p + ds * 16 + hh * 8 + 4, ok);
+    for (int k = 0; k < kQF4; ++k) {
+      const int idx = tid + k * kThreads;
+      qraw[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4, 0, 0));
     }
   }
 
@@ -243,16 +249,24 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
     load_tile(3, Set1{});
     load_tile(4, Set0{});
+    half_t *qt = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kQTileBytes);
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const half4_t lo = round_scaled4(qraw[2 * ds], qscale);
-      const half4_t hi = round_scaled4(qraw[2 * ds + 1], qscale);
-      qf[ds] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    for (int k = 0; k < kQF4; ++k) {
+      const int idx = tid + k * kThreads;
+      *reinterpret_cast<half4_t *>(qt + tile_off(idx >> 4, (idx & 15) * 4)) = round_scaled4(qraw[k], qscale);
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p) store_regs(p, kp[p], vp[p]);
   }
   __syncthreads();
+  {
+    // Q^T fragments (B operand): lane c holds query q_w0 + c, slots d =
+    // 16*ds + 8*hh + j.
+    const half_t *qt = reinterpret_cast<const half_t *>(lds_raw + kLdsBytes - kQTileBytes);
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+      qf[ds] = *reinterpret_cast<const half8_t *>(qt + tile_off(qg * 32 + c, 8 * (2 * ds + hh)));
+  }
   f32x16 s;
   {
     half8_t kf[4];
