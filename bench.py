@@ -157,6 +157,65 @@ def summarize_trace(stats_csv):
     return "\n".join(lines)
 
 
+SEQ_LIMIT_LENGTHS = (8192, 16384, 32768, 65536, 131072, 262144, 524288, 1048576, 2097152)
+
+
+def seq_limit(max_alloc_s):
+    """Forward-only sequence-length sweep (darkforest-core/src/bin/bench_sequence_limit.rs:37-335).
+
+    Same methodology as the reference: H=12, D=64, causal, scale 1/sqrt(64); per S allocate Q, K, V
+    and O (plus the [H, S] lse buffer this build's forward writes), one untimed run when S <= 16384,
+    then 3 (S <= 16384) or 1 timed run with device events, median latency, FLOPs 2*H*S^2*D. Rows
+    above S = 131072 only check that the O(S) allocation succeeds (the reference does not launch
+    them either). Inputs are N(0, 0.5^2) (BASELINE C3). One JSON line per S on stdout.
+    """
+    import torch
+
+    import dfattn
+
+    dev = torch.device("cuda:0")
+    h, d = 12, 64
+    scale = 1.0 / float(np.sqrt(d))
+    log(f"library: {dfattn.version()}  device: {torch.cuda.get_device_name(0)}")
+    for s_len in SEQ_LIMIT_LENGTHS:
+        if s_len > max_alloc_s:
+            break
+        torch.cuda.synchronize()
+        free_before, total = torch.cuda.mem_get_info()
+        gen = torch.Generator(device=dev).manual_seed(4000 + s_len)
+        q, k, v = (torch.randn(s_len, h * d, generator=gen, device=dev) * 0.5 for _ in range(3))
+        o = torch.empty_like(q)
+        lse = torch.empty((h, s_len), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        free_after, _ = torch.cuda.mem_get_info()
+        row = {"seq_len": s_len, "vram_allocated_mb": round((free_before - free_after) / 2 ** 20, 2),
+               "expected_mb": round((4 * s_len * h * d * 4 + h * s_len * 4) / 2 ** 20, 2),
+               "free_vram_mb": round(free_after / 2 ** 20, 1)}
+        if s_len <= 131072:
+            repeats = 3 if s_len <= 16384 else 1
+            if s_len <= 16384:
+                dfattn.attention_forward(q, k, v, h, scale, True, out=o, lse=lse)
+                torch.cuda.synchronize()
+            lat = []
+            for _ in range(repeats):
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record()
+                dfattn.attention_forward(q, k, v, h, scale, True, out=o, lse=lse)
+                ev[1].record()
+                torch.cuda.synchronize()
+                lat.append(ev[0].elapsed_time(ev[1]))
+            med = sorted(lat)[len(lat) // 2]
+            row.update({"latency_ms": round(med, 4), "repeats": repeats,
+                        "tflops": round(2.0 * h * s_len * s_len * d / (med * 1e-3) / 1e12, 2),
+                        "status": "ran"})
+        else:
+            row.update({"latency_ms": None, "tflops": None, "status": "allocation only"})
+        log(f"S={s_len}: {row}")
+        print(json.dumps(row), flush=True)
+        del q, k, v, o, lse
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,7 +233,12 @@ def main():
                     help="print a rocprofv3 --kernel-trace --stats summary table and exit (no GPU)")
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
+    ap.add_argument("--seq-limit", type=int, default=0, metavar="MAX_S",
+                    help="run the reference's forward sequence-length sweep up to MAX_S instead of the C2 bench")
     args = ap.parse_args()
+    if args.seq_limit:
+        seq_limit(args.seq_limit)
+        return
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.copy_calibration or 512))
         return
@@ -271,6 +335,7 @@ def main():
         "bwd_tflops": round(FLOP_BWD / ((pre_ms + main_ms) * 1e-3) / 1e12, 2),
         "step_event_ms_median": round(step_ev_ms[len(step_ev_ms) // 2], 5),
         "step_event_ms_min": round(step_ev_ms[0], 5),
+        "step_event_ms_p90": round(step_ev_ms[min(len(step_ev_ms) - 1, (9 * len(step_ev_ms)) // 10)], 5),
         "roofline": roofline,
         "gpt2_step_ms": None,
     }
