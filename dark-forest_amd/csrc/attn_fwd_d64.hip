@@ -37,17 +37,21 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kD = 64;
 constexpr int kBN = 64;    // keys per LDS tile
 constexpr int kBM = 128;   // query rows per workgroup (4 row groups of 32)
-constexpr int kTile = kBN * kD;           // halves per K or V tile
-constexpr int kStageHalves = 2 * kTile;   // one ring stage: K tile, then V tile
+constexpr int kTile = kBN * kD;  // halves per K or V tile
+constexpr int kTileBytes = kTile * 2;
+// Two LDS rings of kStages stages: K tile t in K stage t % 4, V tile t in V
+// stage t % 4 (the V ring follows the K ring).
 constexpr int kStages = 4;
+constexpr int kVRingBytes = kStages * kTileBytes;
 constexpr int kF4 = kBN * kD / 4 / kThreads;  // float4 of K (and of V) per thread per tile
 static_assert(kF4 * kThreads * 4 == kBN * kD, "tile split");
+static_assert(kThreads * 8 == kTile, "one half8 per thread clears a tile");
 // Merge buffer: per partner wave, 32 output registers + max + sum, lane-major.
 constexpr int kMergeRegs = 34;
 constexpr float kRescale = 8.f;  // log2 headroom of the softmax reference point
-constexpr int kRingBytes = kStages * kStageHalves * 2;
+constexpr int kRingBytes = 2 * kStages * kTileBytes;
 constexpr int kMergeBytes = 4 * kMergeRegs * 64 * 4;
-// After the ring: the workgroup's 128 Q rows as a [128][64] fp16 tile (c2 Q),
+// After the rings: the workgroup's 128 Q rows as a [128][64] fp16 tile (c2 Q),
 // staged once with coalesced loads; each wave reads its fragments from it.
 constexpr int kQTileBytes = kBM * kD * 2;
 constexpr int kQF4 = kBM * kD / 4 / kThreads;  // float4 of Q per thread
@@ -56,12 +60,17 @@ constexpr int kLdsBytes = (kMergeBytes > kRingBytes ? kMergeBytes : kRingBytes) 
 template <int N>
 using Stage = std::integral_constant<int, N>;
 
+// ds_read_b64_tr_b16 at an LDS byte address (lane layout as in tile_tr4).
+__device__ __forceinline__ half4_t lds_tr4(const unsigned char *p) {
+  return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                         (lds_i16x4 *)(const __attribute__((address_space(3))) unsigned char *)p));
+}
+
 __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     float *__restrict__ O, float *__restrict__ LSE, int H, int S, float qscale, int causal,
     int n_qtiles) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
-  half_t *ring = reinterpret_cast<half_t *>(lds_raw);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -106,85 +115,71 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     }
   }
 
-  // Per-thread offsets, fixed for the whole loop (the stage adds a constant):
-  // K rows (A operand of S^T), V^T slots through transposed reads (A operand
-  // of O^T), the thread's share of the tile stores, and its global float4s.
+  // Per-thread byte offsets within a tile, fixed for the whole loop (the
+  // stage adds a constant): K rows (A operand of S^T), V^T slots through
+  // transposed reads (A operand of O^T), the thread's share of a tile store,
+  // and its global float4s.
   int koff[4], voff[2][2][2], soff[kF4], goff[kF4];
 #pragma unroll
-  for (int ds = 0; ds < 4; ++ds) koff[ds] = tile_off(kh * 32 + c, 8 * (2 * ds + hh));
+  for (int ds = 0; ds < 4; ++ds) koff[ds] = 2 * tile_off(kh * 32 + c, 8 * (2 * ds + hh));
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
-        voff[j][db][hf] = tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
+        voff[j][db][hf] = 2 * tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
 #pragma unroll
   for (int i = 0; i < kF4; ++i) {
     const int idx = tid + i * kThreads;
-    soff[i] = tile_off(idx >> 4, (idx & 15) * 4);
+    soff[i] = 2 * tile_off(idx >> 4, (idx & 15) * 4);
     goff[i] = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
   }
 
-  // Tile t of K and V through buffer loads on a descriptor based at key row
-  // 64*t that covers rows up to S-1: rows past the end read as zeros (and are
-  // masked out of the softmax), tiles past the end read as all zeros.
-  // Two register sets of staged K/V float4s (set t % 2 holds tile t), so a
-  // tile is fetched two iterations before it is written to LDS.
+  // LDS stages: K tile t in K stage t % 4, V tile t in V stage t % 4.
+  auto kstage = [&](int t) { return lds_raw + (t & (kStages - 1)) * kTileBytes; };
+  auto vstage = [&](int t) { return lds_raw + kVRingBytes + (t & (kStages - 1)) * kTileBytes; };
+
+  // Rows of tile t of X (K or V) through buffer loads on a descriptor based
+  // at key row 64*t that covers rows up to S-1: rows past the end read as
+  // zeros (and are masked out of the softmax), tiles past the end read as
+  // all zeros. K tile t is staged in kreg[t % 2], V tile t in vreg[t % 2].
   float4 kreg[2][kF4], vreg[2][kF4];
-  auto load_regs = [&](int t, float4 (&kr)[kF4], float4 (&vr)[kF4]) {
+  auto load_rows = [&](const float *X, int t, float4 (&xr)[kF4]) {
     const int kv0 = t * kBN;
     const long long rem = (long long)(S - kv0) * ld * 4;
     const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kBN * ld * 4);
-    const size_t base = (size_t)min(kv0, S) * ld;
-    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(K + base), 0, nrec, kBufferFlags);
-    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(V + base), 0, nrec, kBufferFlags);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)min(kv0, S) * ld), 0, nrec, kBufferFlags);
 #pragma unroll
-    for (int i = 0; i < kF4; ++i) {
-      kr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[i], 0, 0));
-      vr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[i], 0, 0));
-    }
+    for (int i = 0; i < kF4; ++i)
+      xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff[i], 0, 0));
   };
-  auto store_regs = [&](int stage, const float4 (&kr)[kF4], const float4 (&vr)[kF4]) {
-    half_t *kt = ring + stage * kStageHalves;
+  auto store_rows = [&](unsigned char *dst, const float4 (&xr)[kF4]) {
 #pragma unroll
-    for (int i = 0; i < kF4; ++i) {
-      *reinterpret_cast<half4_t *>(kt + soff[i]) = to_half4(kr[i]);
-      *reinterpret_cast<half4_t *>(kt + kTile + soff[i]) = to_half4(vr[i]);
-    }
+    for (int i = 0; i < kF4; ++i) *reinterpret_cast<half4_t *>(dst + soff[i]) = to_half4(xr[i]);
   };
-  auto load_tile = [&](int t, auto set) {
-    constexpr int b = decltype(set)::value;
-    load_regs(t, kreg[b], vreg[b]);
-  };
-  auto store_tile = [&](int stage, auto set) {
-    constexpr int b = decltype(set)::value;
-    store_regs(stage, kreg[b], vreg[b]);
-  };
-  using Set0 = std::integral_constant<int, 0>;
-  using Set1 = std::integral_constant<int, 1>;
 
   f32x16 o[2];
   o[0] = o[1] = f32x16{};
   float m = -INFINITY, l = 0.f;
   f32x16 negm = f32x16{};  // -m_use in every register (m_use = 0 while m = -inf)
 
-  // K rows of this wave's key half (A operand of S^T = K Q^T).
-  auto read_k = [&](int stage, half8_t (&kf)[4]) {
-    const half_t *kt = ring + stage * kStageHalves;
+  // K rows of this wave's key half of tile t (A operand of S^T = K Q^T).
+  auto read_k = [&](int t, half8_t (&kf)[4]) {
+    const unsigned char *kt = kstage(t);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) kf[ds] = *reinterpret_cast<const half8_t *>(kt + koff[ds]);
   };
-  // V^T slots of this wave's two key steps (A operand of O^T += V^T P^T),
-  // whose k-slots follow the row order of P^T.
-  auto read_v = [&](int stage, half8_t (&vf)[2][2]) {
-    const half_t *vt = ring + stage * kStageHalves + kTile;
+  // V^T slots of this wave's two key steps of tile t (A operand of O^T +=
+  // V^T P^T), whose k-slots follow the row order of P^T.
+  auto read_v = [&](int t, half8_t (&vf)[2][2]) {
+    const unsigned char *vt = vstage(t);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
-        const half4_t lo = tile_tr4_at(vt, voff[j][db][0]);
-        const half4_t hi = tile_tr4_at(vt, voff[j][db][1]);
+        const half4_t lo = lds_tr4(vt + voff[j][db][0]);
+        const half4_t hi = lds_tr4(vt + voff[j][db][1]);
         vf[j][db] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
   };
@@ -202,13 +197,39 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   // when a row's maximum exceeds it by more than kRescale, so P^T stays below
   // 2^kRescale (exact in fp16) and the rescale of l and O is rare; m + log2(l)
   // is unchanged by the choice of m. The row sum l adds the same fp16 P the
-  // product uses. `full`: no row of the tile is empty (every lane has a
-  // finite maximum), which shortens the rescale test.
-  auto softmax = [&](f32x16 &s, half8_t (&pf)[2], auto full) {
+  // product uses.
+  //
+  // P^T = exp2(s) is computed before the rescale test is known, so that the
+  // common case runs straight through; the rare rescale recomputes it. `sn`
+  // holds the next tile's scores, already issued against the old reference
+  // point, and O already holds the previous tile's product: a move of m
+  // shifts and rescales them too. `full`: no row of the tile is empty (every
+  // lane has a finite maximum), which shortens the rescale test.
+  // (The empty asm keeps the compiler from merging the speculative and the
+  // recomputed P^T into one computation after the rescale test.)
+  auto probs = [&](const f32x16 &s, half8_t (&pf)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pf[j][i] = (half_t)fast_exp2(s[8 * j + i]);
+      asm volatile("" : "+v"(pf[j]));
+    }
+  };
+  auto row_max = [&](const f32x16 &s) {
     float mx = s[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
-    mx = pair_max(mx);  // row max of S^T - m_use
+    return pair_max(mx);  // row max of S^T - m_use
+  };
+  auto rowsum = [&](const half8_t (&pf)[2]) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) a = sum8_f16(pf[j], a);
+    asm volatile("" : "+v"(a));
+    return a;
+  };
+  // The rescale test and the rare rescale, after row_max, probs and rowsum.
+  auto softmax_fix = [&](f32x16 &s, f32x16 &sn, half8_t (&pf)[2], float mx, float psum, auto full) {
     const bool need = decltype(full)::value ? (mx > kRescale || m == -INFINITY)
                                             : (mx > kRescale || (m == -INFINITY && mx > -INFINITY));
     if (__any(need)) {
@@ -219,19 +240,21 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       l *= alpha;
       o[0] *= alpha;
       o[1] *= alpha;
+      // The reference point moves by `shift` in place (the scores, the
+      // issued next scores and the accumulator input alike); m is read back
+      // from the accumulator input so that lse uses exactly the point the
+      // products were shifted by.
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] -= shift;
-      m = m_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) negm[r] = (m == -INFINITY) ? 0.f : -m;
+      for (int r = 0; r < 16; ++r) {
+        s[r] -= shift;
+        sn[r] -= shift;
+        negm[r] -= shift;
+      }
+      m = (m_new == -INFINITY) ? m_new : -negm[0];
+      probs(s, pf);
+      psum = rowsum(pf);
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      pf[j] = acc_to_slots(s, j);
-      l = sum8_f16(pf[j], l);
-    }
+    l += psum;
   };
   auto pv = [&](const half8_t (&vf)[2][2], const half8_t (&pf)[2]) {
 #pragma unroll
@@ -240,15 +263,30 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       for (int db = 0; db < 2; ++db) o[db] = mfma32x32x16(vf[j][db], pf[j], o[db]);
   };
 
-  // Prologue: every load is issued before the first wait (Q above, tiles 0-2
-  // into prologue registers, tiles 3 and 4 into their sets), then tiles 0-2
-  // go into the ring and S of tile 0 is computed.
+  // Iteration t reads K of tile t+1 (its scores) and V of tile t-1 (the
+  // product of the previous tile's P, one iteration late so that both
+  // products are independent of the softmax of tile t they run beside). It
+  // writes K of tile t+3 and V of tile t+1 into their stages and fetches K of
+  // tile t+5 and V of tile t+3 into the register sets those have just left.
+  // The workgroup synchronises after every second iteration (odd t): what an
+  // iteration writes is read two or more iterations later, and a stage read
+  // in iteration i is next written in iteration i+2, so one barrier always
+  // lies between them.
+  //
+  // Prologue: every load is issued before the first wait (Q above, K tiles
+  // 0-2 and V tile 0 into prologue registers, K tiles 3, 4 and V tiles 1, 2
+  // into their sets), then those go into the rings, the V stage of tile -1
+  // is cleared (tile 0 runs as a steady iteration whose pending product
+  // adds zero) and S of tile 0 is computed.
   {
-    float4 kp[3][kF4], vp[3][kF4];
+    float4 kp[3][kF4], vp[kF4];
 #pragma unroll
-    for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
-    load_tile(3, Set1{});
-    load_tile(4, Set0{});
+    for (int p = 0; p < 3; ++p) load_rows(K, p, kp[p]);
+    load_rows(V, 0, vp);
+    load_rows(K, 3, kreg[1]);
+    load_rows(V, 1, vreg[1]);
+    load_rows(K, 4, kreg[0]);
+    load_rows(V, 2, vreg[0]);
     half_t *qt = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kQTileBytes);
 #pragma unroll
     for (int k = 0; k < kQF4; ++k) {
@@ -256,7 +294,9 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       *reinterpret_cast<half4_t *>(qt + tile_off(idx >> 4, (idx & 15) * 4)) = round_scaled4(qraw[k], qscale);
     }
 #pragma unroll
-    for (int p = 0; p < 3; ++p) store_regs(p, kp[p], vp[p]);
+    for (int p = 0; p < 3; ++p) store_rows(kstage(p), kp[p]);
+    store_rows(vstage(0), vp);
+    *reinterpret_cast<half8_t *>(vstage(-1) + tid * 16) = half8_t{};
   }
   __syncthreads();
   {
@@ -273,23 +313,95 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     read_k(0, kf);
     s = scores(kf);
   }
+  half8_t pprev[2] = {};  // P^T of the previous tile, waiting for its product
 
-  // Steady state, iteration t (stage p = t % 4 a compile-time constant): the
-  // operands of S of tile t+1 and of P V of tile t are read from LDS first,
-  // the softmax of tile t hides their latency, then both products run, tile
-  // t+3 is written into stage (p+3) % 4 (last read in iteration t-1) and tile
-  // t+5 is fetched into the register set tile t+3 has just left.
+  // Whether this wave sees any key of tile t (under causal masking a wave
+  // that sees none of tile t sees none after it).
+  auto active = [&](int t) {
+    const int k0 = t * kBN + kh * 32;  // first key of this wave's half tile
+    return wave_active && k0 < S && (!causal || k0 <= wave_qlast);
+  };
+  // The tile stores and fetches of iteration t, from and into register set
+  // b = (t+1) % 2; q = t mod 4 (a constant in the steady state) places the
+  // stores. `all`: no range checks (the steady state, where K tiles past the
+  // end are fetched as zeros into stages no later iteration reads).
+  auto stage_tiles = [&](int t, int q, auto set, bool all) {
+    constexpr int b = decltype(set)::value;
+    if (all || t + 3 < n_tiles) {
+      store_rows(kstage(q + 3), kreg[b]);
+      if (all || t + 5 < n_tiles) load_rows(K, t + 5, kreg[b]);
+    }
+    if (all || t + 1 < n_tiles) {
+      store_rows(vstage(q + 1), vreg[b]);
+      if (all || t + 3 < n_tiles) load_rows(V, t + 3, vreg[b]);
+    }
+  };
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+
+  // General iteration: runtime stage and register set, masks, tile range
+  // ends. Used for the remainder of the unmasked range and for the tiles
+  // that hold the causal diagonal or the end of the keys.
+  auto step = [&](int t) {
+    const bool act_prev = t >= 1 && active(t - 1);
+    const bool act_cur = active(t);
+    const bool act_next = t + 1 < n_tiles && active(t + 1);
+    half8_t kf[4], vf[2][2], pf[2];
+    f32x16 sn = f32x16{};
+    if (act_next) {
+      read_k(t + 1, kf);
+      sn = scores(kf);
+    }
+    if (act_prev) {
+      read_v(t - 1, vf);
+      pv(vf, pprev);
+    }
+    if (act_cur) {
+      if (t >= n_full) {
+        // Register r holds key t*64 + 32*kh + 4*hh + 8*(r/4) + r%4.
+        const int lim = key_lim - (t * kBN + kh * 32 + hh * 4);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if ((r >> 2) * 8 + (r & 3) > lim) s[r] = -INFINITY;
+      }
+      const float mx = row_max(s);
+      probs(s, pf);
+      softmax_fix(s, sn, pf, mx, rowsum(pf), std::false_type{});
+      s = sn;
+      pprev[0] = pf[0];
+      pprev[1] = pf[1];
+    }
+    if (t & 1)
+      stage_tiles(t, t, Set0{}, false);
+    else
+      stage_tiles(t, t, Set1{}, false);
+    if (t & 1) __syncthreads();
+  };
+
+  // Steady state, iteration t (stage p = t % 4 a compile-time constant, so
+  // every LDS offset is an immediate): unmasked, with a next tile, every
+  // wave active. Both products are issued before the softmax of tile t, and
+  // the tile stores and fetches come before the rare rescale branch, so that
+  // all of it is one block for the scheduler.
   auto iter = [&](int t, auto stage) {
     constexpr int p = decltype(stage)::value;
     half8_t kf[4], vf[2][2], pf[2];
-    read_k((p + 1) & 3, kf);
-    read_v(p, vf);
-    softmax(s, pf, std::true_type{});
-    s = scores(kf);
-    pv(vf, pf);
-    store_tile((p + 3) & 3, std::integral_constant<int, (p + 1) & 1>{});
-    load_tile(t + 5, std::integral_constant<int, (p + 1) & 1>{});
-    __syncthreads();
+    read_k(p + 1, kf);
+    read_v(p + kStages - 1, vf);
+    f32x16 sn = scores(kf);
+    pv(vf, pprev);
+    const float mx = row_max(s);
+    probs(s, pf);
+    const float psum = rowsum(pf);
+    stage_tiles(t, p, std::integral_constant<int, (p + 1) & 1>{}, true);
+    softmax_fix(s, sn, pf, mx, psum, std::true_type{});
+    s = sn;
+    pprev[0] = pf[0];
+    pprev[1] = pf[1];
+    if (p & 1)
+      __syncthreads();
+    else
+      __builtin_amdgcn_sched_barrier(0);  // keep the iterations' register live ranges apart
   };
   int t = 0;
   for (; t + 4 <= n_main; t += 4) {
@@ -298,37 +410,15 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     iter(t + 2, Stage<2>{});
     iter(t + 3, Stage<3>{});
   }
-
-  // Tail: the last (up to three) unmasked tiles of the pipelined range and
-  // the tiles that hold the causal diagonal or the end of the keys.
-  for (; t < n_tiles; ++t) {
-    const int k0 = t * kBN + kh * 32;  // first key of this wave's half tile
-    // Under causal masking a wave that sees none of tile t sees none after it.
-    const bool act = wave_active && k0 < S && (!causal || k0 <= wave_qlast);
-    if (act) {
-      half8_t kf[4], vf[2][2], pf[2];
-      if (t + 1 < n_tiles) read_k((t + 1) & 3, kf);
-      read_v(t & 3, vf);
-      if (t >= n_full) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
-      }
-      softmax(s, pf, std::false_type{});
-      if (t + 1 < n_tiles) s = scores(kf);
-      pv(vf, pf);
-    }
-    if (t + 3 < n_tiles) {
-      if (t & 1) {
-        store_tile((t + 3) & 3, Set0{});
-        if (t + 5 < n_tiles) load_tile(t + 5, Set0{});
-      } else {
-        store_tile((t + 3) & 3, Set1{});
-        if (t + 5 < n_tiles) load_tile(t + 5, Set1{});
-      }
-    }
-    __syncthreads();
+  for (; t < n_tiles; ++t) step(t);
+  // The last tile's product.
+  if (n_tiles > 0 && active(n_tiles - 1)) {
+    half8_t vf[2][2];
+    read_v(n_tiles - 1, vf);
+    pv(vf, pprev);
   }
+  __syncthreads();  // the merge below reuses the rings
+
 
   // Merge the key halves: wave qg+4 hands (o, m, l) to wave qg through LDS.
   float *mbuf = reinterpret_cast<float *>(lds_raw) + (size_t)qg * kMergeRegs * 64;
