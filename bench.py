@@ -67,7 +67,7 @@ def cpu_baseline(heads: int):
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_c2_hbm_traffic.md")
-KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_main_kernel")
+KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_convert_kernel", "bwd_main_kernel")
 
 
 def short_kernel_name(name):
@@ -272,10 +272,10 @@ def main():
         dfattn.attention_forward(q, k, v, H, SCALE, True, out=o, lse=lse)
         if ev is not None:
             ev[1].record(stream)
-        dfattn.backward_preprocess(o, g, ws, H)
+        dfattn.backward_preprocess(q, k, v, o, g, ws, H, SCALE)
         if ev is not None:
             ev[2].record(stream)
-        dfattn.backward_main(q, k, v, g, lse, dq, dk, dv, ws, H, SCALE, True)
+        dfattn.backward_main(q, k, v, o, g, lse, dq, dk, dv, ws, H, SCALE, True)
         if ev is not None:
             ev[3].record(stream)
 

@@ -5,7 +5,7 @@
 //
 // Differences from the reference, all deliberate:
 //  * Every buffer the context needs is allocated at construction (logsumexp
-//    [H, S] and the backward workspace, both O(H*S)); the reference allocates
+//    [H, S] and the backward workspace, O(H*S) and O(H*S*D)); the reference allocates
 //    an H*2*S*S probability scratch on the first backward (lib.rs:2019-2027).
 //  * backward_device_into reuses the O and logsumexp that forward_device_into
 //    wrote when it is called with the same q, k, v pointers (the reference's

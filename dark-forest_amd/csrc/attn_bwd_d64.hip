@@ -102,34 +102,109 @@ constexpr int kQBlock = 64;         // dK/dV workgroup: query rows per step (2 h
 constexpr int kQueriesPerWg = 128;  // dQ workgroup: query rows owned (4 groups of 32)
 constexpr int kKTile = 64;          // dQ workgroup: keys per step (2 halves of 32)
 constexpr int kTile = 64 * kD;      // halves per staged [64][64] tile
-constexpr int kStageF4 = 64 * kD / 4 / kThreads;  // float4 per thread per staged tile
-static_assert(kStageF4 * kThreads * 4 == 64 * kD, "staging split");
+// fp16 copies are staged one 16-byte granule (8 halves) per thread per
+// [64][64] tile: thread t takes row t/8, granule t%8.
+static_assert(64 * kD / 8 == kThreads, "one granule per thread per staged tile");
 // LDS ring of kStages stages, each two fp16 tiles (Q and dO, or K and V) and,
 // for the dK/dV path, the block's two row statistics. After the loop the same
-// bytes carry the partner waves' partial results (4 waves x 32 registers x 64
+// bytes carry the partner waves' partial results (8 waves x 32 registers x 64
 // lanes fp32).
 constexpr int kStages = 4;
 constexpr int kStageBytes = 2 * kTile * 2 + 2 * kQBlock * 4;
 constexpr int kRingBytes = kStages * kStageBytes;
-constexpr int kMergeBytes = 4 * 32 * 64 * 4;
+constexpr int kMergeBytes = 8 * 32 * 64 * 4;
 // After the ring: the workgroup's own 128 rows of K and V (dK/dV path) or of
 // c2*Q and sigma*dO (dQ path) as two [128][64] fp16 tiles, staged once with
 // coalesced loads; each wave reads its register fragments from there.
 constexpr int kOwnTile = 128 * kD;  // halves
 constexpr int kOwnBytes = 2 * kOwnTile * 2;
-constexpr int kOwnF4 = 128 * kD / 4 / kThreads;  // float4 per thread per own tile
+constexpr int kOwnG = 128 * kD / 8 / kThreads;  // granules per thread per own tile
 constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes;
 
 template <int N>
 using Const = std::integral_constant<int, N>;
+
+// Workspace layout (bytes): Delta [H*S] fp32 | dO block max [H*ceil(S/64)]
+// fp32 | then, 256-byte aligned, the fp16 copies c2*Q, K, V and sigma*dO,
+// each [H][S][64].
+struct WsLayout {
+  size_t blockmax, q16, k16, v16, do16, total;
+};
+inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+inline WsLayout ws_layout(int H, int S) {
+  WsLayout w;
+  w.blockmax = ws_delta_floats(H, S) * sizeof(float);
+  const size_t copy = align256((size_t)H * S * kD * sizeof(half_t));
+  w.q16 = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
+  w.k16 = w.q16 + copy;
+  w.v16 = w.k16 + copy;
+  w.do16 = w.v16 + copy;
+  w.total = w.do16 + copy;
+  return w;
+}
+
+// fp16 copies for the main kernel: 64 rows of one head per workgroup (256
+// threads; thread t converts row t/4, columns 16*(t%4) .. +15 of each
+// tensor). c2*Q is rounded as the forward rounds its Q (round_scaled4);
+// sigma is the head's power of two from the preprocess block maxima, so
+// sigma*dO is exact in fp32 and rounds as the preprocess rounded it for
+// Delta wherever sigma*dO is an fp16 normal number.
+__global__ __launch_bounds__(256) void bwd_convert_kernel(
+    const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
+    const float *__restrict__ dO, const float *__restrict__ blockmax, half_t *__restrict__ q16,
+    half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16, int H, int S,
+    int n_pre_blocks, float c2) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int head = blockIdx.y;
+  const int row = blockIdx.x * 64 + (tid >> 2);
+  const bool ok = row < S;
+  const size_t src = ok ? (size_t)row * H * kD + (size_t)head * kD + (tid & 3) * 16 : 0;
+  const size_t dst = ((size_t)head * S + row) * kD + (tid & 3) * 16;
+  // Every load first, then sigma of the head (from the preprocess block
+  // maxima, reduced by every wave), then the conversions.
+  float4 x[4][4];
+  const float *in[4] = {Q, K, V, dO};
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok);
+  float gmax = 0.f;
+  for (int i = lane; i < n_pre_blocks; i += 64) gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
+  const float sigma = pow2_scale(wave_max(gmax));
+  if (!ok) return;
+  half_t *out[4] = {q16, k16, v16, do16};
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      half4_t lo, hi;
+      if (t == 0) {
+        lo = round_scaled4(x[t][2 * i], c2);
+        hi = round_scaled4(x[t][2 * i + 1], c2);
+      } else if (t == 3) {
+        lo = to_half4(scale4(x[t][2 * i], sigma));
+        hi = to_half4(scale4(x[t][2 * i + 1], sigma));
+      } else {
+        lo = to_half4(x[t][2 * i]);
+        hi = to_half4(x[t][2 * i + 1]);
+      }
+      *reinterpret_cast<half8_t *>(out[t] + dst + 8 * i) =
+          half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+}
 
 // Relative cost of one step of each item kind (measured at C2: a dK/dV step,
 // four products over a 64-row block, takes about 1.3 times a dQ step).
 constexpr int kCostKvStep = 32;
 constexpr int kCostQStep = 25;
 
+// The main kernel reads fp16 copies of its inputs, written once by
+// bwd_convert_kernel in [H][S][64] order: c2*Q (c2 = scale*log2(e), the
+// forward's rounding), K, V and sigma*dO (sigma the head's power-of-two
+// scale).
 struct BwdArgs {
-  const float *Q, *K, *V, *dO, *LSE, *delta, *blockmax;
+  const half_t *Q16, *K16, *V16, *dO16;
+  const float *LSE, *delta, *blockmax;
   float *dQ, *dK, *dV;
   int H, S, causal, n_pre_blocks;
   float scale;
@@ -147,27 +222,65 @@ __device__ __forceinline__ float head_blockmax(const BwdArgs &a, int head, int l
 }
 __device__ __forceinline__ float head_sigma(float lane_max) { return pow2_scale(wave_max(lane_max)); }
 
+// Loads from an fp16 copy ([H][S][64], 128-byte rows) through a buffer
+// descriptor that covers rows row0 .. min(row0 + n, S) - 1 of the head:
+// rows past S read as zeros. Thread t takes the 16-byte granules t, t + 512,
+// .. of the rows (row idx/8, granule idx%8), so each wave reads 1 KB runs.
+template <int NRows>
+__device__ __forceinline__ auto rows16_rsrc(const half_t *p, int head, int S, int row0) {
+  const unsigned nrec = (unsigned)max(0, min(S - row0, NRows)) * kD * 2;
+  return buffer_rsrc(p + ((size_t)head * S + min(row0, S)) * kD, nrec);
+}
+// This thread's granule of the 64 rows from row0.
+__device__ __forceinline__ half8_t load_granule16(const half_t *p, int head, int S, int row0) {
+  const auto rs = rows16_rsrc<64>(p, head, S, row0);
+  return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16, 0, 0));
+}
+// This thread's two granules of the 128 rows from row0.
+__device__ __forceinline__ void load_rows16(const half_t *p, int head, int S, int row0, half8_t (&g)[kOwnG]) {
+  const auto rs = rows16_rsrc<128>(p, head, S, row0);
+#pragma unroll
+  for (int k = 0; k < kOwnG; ++k)
+    g[k] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x + k * kThreads) * 16, 0, 0));
+}
+// The granules of load_rows16 into a swizzled [128][64] tile.
+__device__ __forceinline__ void store_rows16(half_t *tile, const half8_t (&g)[kOwnG]) {
+#pragma unroll
+  for (int k = 0; k < kOwnG; ++k) {
+    const int idx = threadIdx.x + k * kThreads;
+    *reinterpret_cast<half8_t *>(tile + tile_off(idx >> 3, (idx & 7) * 8)) = g[k];
+  }
+}
+
 // Partner waves (w, w+4) hold partial sums of the same 32x32 accumulator
-// blocks: wave w+4 hands its two blocks to wave w through LDS (after a
-// barrier that ends all use of the staging tiles), wave w adds them.
-__device__ __forceinline__ void merge_pair(float *buf, int wave, int lane, f32x16 &x0, f32x16 &x1) {
-  float *mine = buf + (size_t)(wave & 3) * 32 * 64;
-  if (wave >= 4) {
+// blocks. Each hands the N blocks it gives up to the other through LDS and
+// adds the N it keeps from the other's slot, so both halves of the final
+// sums (and of the output stores) are finished in parallel. LDS slot of wave
+// w: 4N groups of 4 registers x 64 lanes, one 16-byte store per group and
+// lane. The caller has ended all use of the staging tiles (a barrier) before;
+// the buffer is not reused after.
+template <int N>
+__device__ __forceinline__ void exchange_pair(float *buf, int wave, int lane, f32x16 (&keep)[N],
+                                              const f32x16 (&give)[N]) {
+  float4 *mine = reinterpret_cast<float4 *>(buf) + (size_t)wave * 4 * N * 64;
+  const float4 *theirs = reinterpret_cast<const float4 *>(buf) + (size_t)(wave ^ 4) * 4 * N * 64;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      mine[r * 64 + lane] = x0[r];
-      mine[(16 + r) * 64 + lane] = x1[r];
-    }
-  }
-  __syncthreads();
-  if (wave < 4) {
+  for (int n = 0; n < N; ++n)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      x0[r] += mine[r * 64 + lane];
-      x1[r] += mine[(16 + r) * 64 + lane];
-    }
-  }
+    for (int g = 0; g < 4; ++g)
+      mine[(4 * n + g) * 64 + lane] =
+          make_float4(give[n][4 * g], give[n][4 * g + 1], give[n][4 * g + 2], give[n][4 * g + 3]);
   __syncthreads();
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 v = theirs[(4 * n + g) * 64 + lane];
+      keep[n][4 * g] += v.x;
+      keep[n][4 * g + 1] += v.y;
+      keep[n][4 * g + 2] += v.z;
+      keep[n][4 * g + 3] += v.w;
+    }
 }
 
 // dK and dV of keys [kv_blk0, kv_blk0 + 128) of one head. Wave w owns keys
@@ -187,7 +300,6 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int S = a.S;
   const int ld = a.H * kD, hoff = head * kD;
   const float bmax = head_blockmax(a, head, lane);
-  const float c2 = a.scale * kLog2e;
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
   const int key = key0 + c;
 
@@ -196,20 +308,9 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // (Read from the workgroup's K/V tiles after the prologue; the rows of keys
   // kv_blk0 .. +127 are fetched with coalesced buffer loads first.)
   half8_t kf[4], vf[4];
-  float4 kown[kOwnF4], vown[kOwnF4];
-  {
-    const unsigned rows = (unsigned)max(0, min(S - kv_blk0, 128));
-    const size_t base = (size_t)min(kv_blk0, S) * ld;
-    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(a.K + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
-    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.V + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
-#pragma unroll
-    for (int k = 0; k < kOwnF4; ++k) {
-      const int idx = tid + k * kThreads;
-      const int off = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
-      kown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-      vown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-    }
-  }
+  half8_t kown[kOwnG], vown[kOwnG];
+  load_rows16(a.K16, head, S, kv_blk0, kown);
+  load_rows16(a.V16, head, S, kv_blk0, vown);
 
   const int n_qblocks = (S + kQBlock - 1) / kQBlock;
   const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
@@ -222,7 +323,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // Per-thread offsets, fixed for the whole loop: rows qh*32 + c of a tile
   // (A operands of S and dP), this wave's transposed reads (B operands of dV
   // and dK), the thread's share of the tile stores and its global float4s.
-  int roff[4], troff[2][2][2], soff[kStageF4], goff[kStageF4];
+  int roff[4], troff[2][2][2];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) roff[ds] = tile_off(qh * 32 + c, 8 * (2 * ds + hh));
 #pragma unroll
@@ -232,52 +333,34 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         troff[j][db][hf] = tile_tr4_off(16 * (2 * qh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-#pragma unroll
-  for (int k = 0; k < kStageF4; ++k) {
-    const int idx = tid + k * kThreads;
-    soff[k] = tile_off(idx >> 4, (idx & 15) * 4);
-    goff[k] = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
-  }
+  const int soff = tile_off(tid >> 3, (tid & 7) * 8);  // this thread's granule of a staged tile
 
   auto stage_base = [&](int st) { return lds_raw + st * kStageBytes; };
-  // Staged rows of Q and dO (buffer loads on a descriptor based at the
-  // block's first row: rows past S read as zeros) and the block's lse and
-  // Delta (lane = row; every wave loads and stores the same 64 values).
-  float4 qreg[2][kStageF4], greg[2][kStageF4];
+  // Staged rows of c2*Q and sigma*dO (one granule per thread; rows past S
+  // read as zeros) and the block's lse and Delta (lane = row; every wave
+  // loads and stores the same 64 values).
+  half8_t qreg[2], greg[2];
   float lraw[2], draw[2];
-  auto load_regs = [&](int i, float4 (&qr)[kStageF4], float4 (&gr)[kStageF4], float &lr, float &dr) {
+  auto load_regs = [&](int i, half8_t &qr, half8_t &gr, float &lr, float &dr) {
     const int qb0 = (first_qb + i) * kQBlock;
-    const long long rem = (long long)(S - qb0) * ld * 4;
-    const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kQBlock * ld * 4);
-    const size_t base = (size_t)min(qb0, S) * ld;
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + base), 0, nrec, kBufferFlags);
-    const auto rg = __builtin_amdgcn_make_buffer_rsrc((void *)(a.dO + base), 0, nrec, kBufferFlags);
-#pragma unroll
-    for (int k = 0; k < kStageF4; ++k) {
-      qr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, goff[k], 0, 0));
-      gr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff[k], 0, 0));
-    }
+    qr = load_granule16(a.Q16, head, S, qb0);
+    gr = load_granule16(a.dO16, head, S, qb0);
     const unsigned srec = (unsigned)max(0, min(S - qb0, kQBlock)) * 4;
     const size_t sbase = (size_t)head * S + min(qb0, S);
-    const auto rl = __builtin_amdgcn_make_buffer_rsrc((void *)(a.LSE + sbase), 0, srec, kBufferFlags);
-    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void *)(a.delta + sbase), 0, srec, kBufferFlags);
+    const auto rl = buffer_rsrc(a.LSE + sbase, srec);
+    const auto rd = buffer_rsrc(a.delta + sbase, srec);
     lr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0));
     dr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, lane * 4, 0, 0));
   };
-  // Q is rounded as c2*Q (the forward's rounding), dO as sigma*dO; the
-  // statistics are stored negated (they enter the products as accumulator
-  // inputs), rows past S get lse = +inf so that P = 0.
+  // The statistics are stored negated (they enter the products as
+  // accumulator inputs), rows past S get lse = +inf so that P = 0.
   float sigma = 1.f;
-  auto store_regs = [&](int i, int st, const float4 (&qr)[kStageF4], const float4 (&gr)[kStageF4], float lr,
-                        float dr) {
+  auto store_regs = [&](int i, int st, const half8_t &qr, const half8_t &gr, float lr, float dr) {
     half_t *qt = reinterpret_cast<half_t *>(stage_base(st));
     half_t *gt = qt + kTile;
     float *sl = reinterpret_cast<float *>(gt + kTile);
-#pragma unroll
-    for (int k = 0; k < kStageF4; ++k) {
-      *reinterpret_cast<half4_t *>(qt + soff[k]) = round_scaled4(qr[k], c2);
-      *reinterpret_cast<half4_t *>(gt + soff[k]) = to_half4(scale4(gr[k], sigma));
-    }
+    *reinterpret_cast<half8_t *>(qt + soff) = qr;
+    *reinterpret_cast<half8_t *>(gt + soff) = gr;
     const int row = (first_qb + i) * kQBlock + lane;
     sl[lane] = row < S ? -lr * kLog2e : -INFINITY;
     sl[kQBlock + lane] = -(dr * sigma);
@@ -379,7 +462,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // read zeros into stages that are never read), then sigma, then blocks 0-2
   // go into the ring.
   {
-    float4 qp[3][kStageF4], gp[3][kStageF4];
+    half8_t qp[3], gp[3];
     float lp[3], dpr[3];
 #pragma unroll
     for (int p = 0; p < 3; ++p) load_regs(p, qp[p], gp[p], lp[p], dpr[p]);
@@ -387,12 +470,8 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     load_block(4, Const<0>{});
     sigma = head_sigma(bmax);
     half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
-#pragma unroll
-    for (int k = 0; k < kOwnF4; ++k) {
-      const int idx = tid + k * kThreads;
-      *reinterpret_cast<half4_t *>(own + tile_off(idx >> 4, (idx & 15) * 4)) = to_half4(kown[k]);
-      *reinterpret_cast<half4_t *>(own + kOwnTile + tile_off(idx >> 4, (idx & 15) * 4)) = to_half4(vown[k]);
-    }
+    store_rows16(own, kown);
+    store_rows16(own + kOwnTile, vown);
 #pragma unroll
     for (int p = 0; p < 3; ++p) store_regs(p, (p - i0) & 3, qp[p], gp[p], lp[p], dpr[p]);
   }
@@ -427,25 +506,25 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   }
   for (; i < nb; ++i) step(i, false);
 
+  // Wave w finishes dK and wave w+4 dV of the same 32 keys.
   float *buf = reinterpret_cast<float *>(lds_raw);
-  merge_pair(buf, wave, lane, dk[0], dk[1]);
-  merge_pair(buf, wave, lane, dv[0], dv[1]);
-  if (wave >= 4) return;
+  if (qh == 0)
+    exchange_pair<2>(buf, wave, lane, dk, dv);
+  else
+    exchange_pair<2>(buf, wave, lane, dv, dk);
 
   // dK = scale * dS^T Q = ln2 * dS^T (c2 Q) / sigma, dV = P^T dO / sigma; row
   // r is key key0 + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
-  const float dk_scale = kLn2 / sigma, dv_scale = 1.f / sigma;
+  const f32x16 *res = qh == 0 ? dk : dv;
+  float *out = qh == 0 ? a.dK : a.dV;
+  const float out_scale = qh == 0 ? kLn2 / sigma : 1.f / sigma;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int kr = key0 + (r >> 2) * 8 + hh * 4 + (r & 3);
     if (kr < S) {
-      float *dkrow = a.dK + (size_t)kr * ld + hoff;
-      float *dvrow = a.dV + (size_t)kr * ld + hoff;
+      float *row = out + (size_t)kr * ld + hoff;
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        dkrow[db * 32 + c] = dk[db][r] * dk_scale;
-        dvrow[db * 32 + c] = dv[db][r] * dv_scale;
-      }
+      for (int db = 0; db < 2; ++db) row[db * 32 + c] = res[db][r] * out_scale;
     }
   }
 }
@@ -459,7 +538,6 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int S = a.S;
   const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
   const float bmax = head_blockmax(a, head, lane);
-  const float c2 = a.scale * kLog2e;
   const int q_w0 = q_blk0 + qg * 32;
   const int query = q_w0 + c;
   const bool q_ok = query < S;
@@ -470,23 +548,13 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int key_lim = a.causal ? min(query, S - 1) : S - 1;
   const int key_lim_lo = a.causal ? min(q_w0, S - 1) : S - 1;
 
-  // Raw Q / dO rows and row statistics of the lane's query; they become the
-  // (c2 Q)^T and (sigma dO)^T fragments (B operands, lane c holds its query)
-  // once sigma is known, after the prologue has issued every load.
-  float4 qown[kOwnF4], gown[kOwnF4];
-  {
-    const unsigned rows = (unsigned)max(0, min(S - q_blk0, 128));
-    const size_t base = (size_t)min(q_blk0, S) * ld;
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(a.Q + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
-    const auto rg = __builtin_amdgcn_make_buffer_rsrc((void *)(a.dO + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
-#pragma unroll
-    for (int k = 0; k < kOwnF4; ++k) {
-      const int idx = tid + k * kThreads;
-      const int off = (int)(((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4);
-      qown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0));
-      gown[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
-    }
-  }
+  // The workgroup's c2*Q and sigma*dO rows and the lane's row statistics;
+  // the rows become the (c2 Q)^T and (sigma dO)^T fragments (B operands,
+  // lane c holds its query) through LDS, after the prologue has issued every
+  // load.
+  half8_t qown[kOwnG], gown[kOwnG];
+  load_rows16(a.Q16, head, S, q_blk0, qown);
+  load_rows16(a.dO16, head, S, q_blk0, gown);
   const float Lraw = q_ok ? a.LSE[(size_t)head * S + query] : 0.f;
   const float Draw = q_ok ? a.delta[(size_t)head * S + query] : 0.f;
   half8_t qf[4], gf[4];
@@ -503,7 +571,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // Per-thread offsets: K/V rows kh*32 + c (A operands of S^T and dP^T), K^T
   // slots through transposed reads (A operand of dQ^T), tile stores and the
   // thread's global float4s.
-  int koff[4], ktoff[2][2][2], soff[kStageF4], goff[kStageF4];
+  int koff[4], ktoff[2][2][2];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) koff[ds] = tile_off(kh * 32 + c, 8 * (2 * ds + hh));
 #pragma unroll
@@ -513,39 +581,22 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         ktoff[j][db][hf] = tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-#pragma unroll
-  for (int k = 0; k < kStageF4; ++k) {
-    const int idx = tid + k * kThreads;
-    soff[k] = tile_off(idx >> 4, (idx & 15) * 4);
-    goff[k] = ((idx >> 4) * (int)ld + (int)hoff + (idx & 15) * 4) * 4;
-  }
+  const int soff = tile_off(tid >> 3, (tid & 7) * 8);  // this thread's granule of a staged tile
 
   // Tile t goes through ring stage t % 4 and register set t % 2; tile t+3
   // is written during iteration t (into the stage last read in iteration
   // t-1) and tile t+5 is fetched into the set tile t+3 has just left. Keys
   // past S read as zeros and are masked to P = 0.
   auto stage_base = [&](int st) { return reinterpret_cast<half_t *>(lds_raw + st * kStageBytes); };
-  float4 kreg[2][kStageF4], vreg[2][kStageF4];
-  auto load_regs = [&](int t, float4 (&kr)[kStageF4], float4 (&vr)[kStageF4]) {
-    const int kv0 = t * kKTile;
-    const long long rem = (long long)(S - kv0) * (long long)ld * 4;
-    const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kKTile * (long long)ld * 4);
-    const size_t base = (size_t)min(kv0, S) * ld;
-    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(a.K + base), 0, nrec, kBufferFlags);
-    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.V + base), 0, nrec, kBufferFlags);
-#pragma unroll
-    for (int k = 0; k < kStageF4; ++k) {
-      kr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, goff[k], 0, 0));
-      vr[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, goff[k], 0, 0));
-    }
+  half8_t kreg[2], vreg[2];
+  auto load_regs = [&](int t, half8_t &kr, half8_t &vr) {
+    kr = load_granule16(a.K16, head, S, t * kKTile);
+    vr = load_granule16(a.V16, head, S, t * kKTile);
   };
-  auto store_regs = [&](int st, const float4 (&kr)[kStageF4], const float4 (&vr)[kStageF4]) {
+  auto store_regs = [&](int st, const half8_t &kr, const half8_t &vr) {
     half_t *kt = stage_base(st);
-#pragma unroll
-    for (int k = 0; k < kStageF4; ++k) {
-      *reinterpret_cast<half4_t *>(kt + soff[k]) = to_half4(kr[k]);
-      *reinterpret_cast<half4_t *>(kt + kTile + soff[k]) = to_half4(vr[k]);
-    }
+    *reinterpret_cast<half8_t *>(kt + soff) = kr;
+    *reinterpret_cast<half8_t *>(kt + kTile + soff) = vr;
   };
   auto load_tile = [&](int t, auto set) {
     constexpr int b = decltype(set)::value;
@@ -609,20 +660,15 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // prologue registers, tiles 3 and 4 into their sets), then sigma and the
   // fragments, then tiles 0-2 go into the ring.
   {
-    float4 kp[3][kStageF4], vp[3][kStageF4];
+    half8_t kp[3], vp[3];
 #pragma unroll
     for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
     load_tile(3, Const<1>{});
     load_tile(4, Const<0>{});
     sigma = head_sigma(bmax);
     half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
-#pragma unroll
-    for (int k = 0; k < kOwnF4; ++k) {
-      const int idx = tid + k * kThreads;
-      *reinterpret_cast<half4_t *>(own + tile_off(idx >> 4, (idx & 15) * 4)) = round_scaled4(qown[k], c2);
-      *reinterpret_cast<half4_t *>(own + kOwnTile + tile_off(idx >> 4, (idx & 15) * 4)) =
-          to_half4(scale4(gown[k], sigma));
-    }
+    store_rows16(own, qown);
+    store_rows16(own + kOwnTile, gown);
     const float L = q_ok ? Lraw * kLog2e : INFINITY;
     const float Dl = Draw * sigma;
 #pragma unroll
@@ -673,20 +719,21 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     __syncthreads();
   }
 
-  merge_pair(reinterpret_cast<float *>(lds_raw), wave, lane, dq[0], dq[1]);
-  if (wave >= 4) return;
+  // Wave w finishes columns 0-31 of dQ and wave w+4 columns 32-63 of the
+  // same 32 rows (each gives up the other block).
+  f32x16 res[1] = {kh == 0 ? dq[0] : dq[1]};
+  const f32x16 give[1] = {kh == 0 ? dq[1] : dq[0]};
+  exchange_pair<1>(reinterpret_cast<float *>(lds_raw), wave, lane, res, give);
 
   // dQ = scale * dS K / sigma; register r of block db is column 32*db + 8*(r/4) + 4*hh + r%4.
   if (q_ok) {
     const float dq_scale = a.scale / sigma;
-    float *qrow = a.dQ + (size_t)query * ld + hoff;
+    float *qrow = a.dQ + (size_t)query * ld + hoff + kh * 32;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4 *>(qrow + db * 32 + g * 8 + hh * 4) =
-            make_float4(dq[db][4 * g] * dq_scale, dq[db][4 * g + 1] * dq_scale,
-                        dq[db][4 * g + 2] * dq_scale, dq[db][4 * g + 3] * dq_scale);
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4 *>(qrow + g * 8 + hh * 4) =
+          make_float4(res[0][4 * g] * dq_scale, res[0][4 * g + 1] * dq_scale, res[0][4 * g + 2] * dq_scale,
+                      res[0][4 * g + 3] * dq_scale);
   }
 }
 
@@ -745,6 +792,11 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
   } else {
     sched.pick(b / a.H, kv_item, rank);
   }
+  // The item is the same for the whole workgroup; saying so keeps every
+  // address and buffer descriptor derived from it in scalar registers (the
+  // table entry arrives through a vector load).
+  rank = __builtin_amdgcn_readfirstlane(rank);
+  kv_item = __builtin_amdgcn_readfirstlane(kv_item ? 1 : 0) != 0;
   const int head = b % a.H;
   if (kv_item) {
     dkdv_path(a, head, rank * kKeysPerWg, lds_raw);
@@ -756,32 +808,37 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
 
 }  // namespace
 
-size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) {
-  const size_t floats = ws_delta_floats(n_heads, seq_len) + (size_t)n_heads * pre_blocks(seq_len);
-  return (floats * sizeof(float) + 255) / 256 * 256;
-}
+size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) { return ws_layout(n_heads, seq_len).total; }
 
-hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, void *workspace, int n_heads,
-                              int seq_len, hipStream_t stream) {
-  float *delta = static_cast<float *>(workspace);
-  float *blockmax = delta + ws_delta_floats(n_heads, seq_len);
+hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
+                              const float *d_o, void *workspace, int n_heads, int seq_len, float scale,
+                              hipStream_t stream) {
+  const WsLayout w = ws_layout(n_heads, seq_len);
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  float *delta = reinterpret_cast<float *>(ws);
+  float *blockmax = reinterpret_cast<float *>(ws + w.blockmax);
   hipLaunchKernelGGL(bwd_preprocess_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream,
                      o, d_o, delta, blockmax, n_heads, seq_len);
+  if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
+  hipLaunchKernelGGL(bwd_convert_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v,
+                     d_o, blockmax, reinterpret_cast<half_t *>(ws + w.q16), reinterpret_cast<half_t *>(ws + w.k16),
+                     reinterpret_cast<half_t *>(ws + w.v16), reinterpret_cast<half_t *>(ws + w.do16), n_heads,
+                     seq_len, pre_blocks(seq_len), scale * kLog2e);
   return hipGetLastError();
 }
 
-hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, const float *d_o,
-                               const float *lse, float *d_q, float *d_k, float *d_v,
-                               const void *workspace, int n_heads, int seq_len, float scale,
-                               bool causal, hipStream_t stream) {
+hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
+                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream) {
+  const WsLayout w = ws_layout(n_heads, seq_len);
+  const unsigned char *ws = static_cast<const unsigned char *>(workspace);
   BwdArgs a;
-  a.Q = q;
-  a.K = k;
-  a.V = v;
-  a.dO = d_o;
+  a.Q16 = reinterpret_cast<const half_t *>(ws + w.q16);
+  a.K16 = reinterpret_cast<const half_t *>(ws + w.k16);
+  a.V16 = reinterpret_cast<const half_t *>(ws + w.v16);
+  a.dO16 = reinterpret_cast<const half_t *>(ws + w.do16);
   a.LSE = lse;
-  a.delta = static_cast<const float *>(workspace);
-  a.blockmax = a.delta + ws_delta_floats(n_heads, seq_len);
+  a.delta = reinterpret_cast<const float *>(ws);
+  a.blockmax = reinterpret_cast<const float *>(ws + w.blockmax);
   a.dQ = d_q;
   a.dK = d_k;
   a.dV = d_v;
@@ -817,10 +874,9 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
                           bool causal, hipStream_t stream) {
-  hipError_t err = launch_bwd_pre_d64(o, d_o, workspace, n_heads, seq_len, stream);
+  hipError_t err = launch_bwd_pre_d64(q, k, v, o, d_o, workspace, n_heads, seq_len, scale, stream);
   if (err != hipSuccess) return err;
-  return launch_bwd_main_d64(q, k, v, d_o, lse, d_q, d_k, d_v, workspace, n_heads, seq_len, scale,
-                             causal, stream);
+  return launch_bwd_main_d64(lse, d_q, d_k, d_v, workspace, n_heads, seq_len, scale, causal, stream);
 }
 
 }  // namespace dfattn

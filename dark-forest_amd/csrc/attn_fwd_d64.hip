@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   {
     const unsigned rows = (unsigned)max(0, min(S - q_blk0, kBM));
     const size_t base = (size_t)min(q_blk0, S) * ld;
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(Q + base), 0, rows * (unsigned)ld * 4, kBufferFlags);
+    const auto rq = buffer_rsrc(Q + base, rows * (unsigned)ld * 4);
 #pragma unroll
     for (int k = 0; k < kQF4; ++k) {
       const int idx = tid + k * kThreads;
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const int kv0 = t * kBN;
     const long long rem = (long long)(S - kv0) * ld * 4;
     const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kBN * ld * 4);
-    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)min(kv0, S) * ld), 0, nrec, kBufferFlags);
+    const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ld, nrec);
 #pragma unroll
     for (int i = 0; i < kF4; ++i)
       xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff[i], 0, 0));

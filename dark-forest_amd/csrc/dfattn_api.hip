@@ -241,35 +241,38 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o, c
   return record_hip(err, "attention backward launch");
 }
 
-int dfattn_bwd_preprocess(const float *o, const float *d_o, void *workspace,
-                          size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
-                          uint32_t d_head, void *stream) {
+// The split backward decides the fast path from q, k, v, o and d_o in both
+// phases, so main takes it only when preprocess filled the workspace.
+int dfattn_bwd_preprocess(const float *q, const float *k, const float *v, const float *o,
+                          const float *d_o, void *workspace, size_t workspace_bytes,
+                          uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale,
+                          void *stream) {
   const char *fn = "dfattn_bwd_preprocess";
   int st = check_shape(fn, n_heads, seq_len, d_head);
-  if (st == DFATTN_OK) st = check_ptrs(fn, {o, d_o});
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o});
   if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
   if (st != DFATTN_OK) return st;
   // The generic kernel recomputes its row statistics itself: nothing to do.
-  if (!fast_path(d_head, {o, d_o})) return DFATTN_OK;
-  return record_hip(dfattn::launch_bwd_pre_d64(o, d_o, workspace, (int)n_heads, (int)seq_len,
-                                               static_cast<hipStream_t>(stream)),
+  if (!fast_path(d_head, {q, k, v, o, d_o})) return DFATTN_OK;
+  return record_hip(dfattn::launch_bwd_pre_d64(q, k, v, o, d_o, workspace, (int)n_heads, (int)seq_len,
+                                               scale, static_cast<hipStream_t>(stream)),
                     "attention backward preprocess launch");
 }
 
-int dfattn_bwd_main(const float *q, const float *k, const float *v, const float *d_o,
-                    const float *lse, float *d_q, float *d_k, float *d_v, void *workspace,
-                    size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
-                    float scale, uint32_t causal, void *stream) {
+int dfattn_bwd_main(const float *q, const float *k, const float *v, const float *o,
+                    const float *d_o, const float *lse, float *d_q, float *d_k, float *d_v,
+                    void *workspace, size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
+                    uint32_t d_head, float scale, uint32_t causal, void *stream) {
   const char *fn = "dfattn_bwd_main";
   int st = check_shape(fn, n_heads, seq_len, d_head);
-  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, d_o, lse, d_q, d_k, d_v});
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse, d_q, d_k, d_v});
   if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
   if (st != DFATTN_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
-  if (fast_path(d_head, {q, k, v, d_o, lse, d_q, d_k, d_v}))
-    err = dfattn::launch_bwd_main_d64(q, k, v, d_o, lse, d_q, d_k, d_v, workspace, (int)n_heads,
-                                      (int)seq_len, scale, causal != 0, s);
+  if (fast_path(d_head, {q, k, v, o, d_o}) && fast_path(d_head, {lse, d_q, d_k, d_v}))
+    err = dfattn::launch_bwd_main_d64(lse, d_q, d_k, d_v, workspace, (int)n_heads, (int)seq_len, scale,
+                                      causal != 0, s);
   else
     err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
                                      (int)d_head, scale, causal != 0, s);

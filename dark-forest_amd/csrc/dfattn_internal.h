@@ -20,6 +20,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Word 3 of a raw buffer descriptor (gfx9 family: 32-bit data format, no
 // swizzle); loads past num_records return zeros.
 constexpr int kBufferFlags = 0x00020000;
+
+// Raw buffer descriptor over nrec bytes from p. The kernels build descriptors
+// only from workgroup-uniform values; readfirstlane states that, which keeps
+// the descriptor in scalar registers (a clamp the compiler lowers to a vector
+// med3 would otherwise move it to vector registers and wrap every load in a
+// loop over the lanes' distinct descriptors).
+__device__ __forceinline__ auto buffer_rsrc(const void *p, unsigned nrec) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, __builtin_amdgcn_readfirstlane(nrec),
+                                           kBufferFlags);
+}
 constexpr float kLn2 = 0.6931471805599453f;
 
 // D = 64 fast path: one 32x32x16 fp16 MFMA (fp32 accumulate). Operand
@@ -190,13 +200,14 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
                           bool causal, hipStream_t stream);
-// The two phases of launch_bwd_d64: Delta and the dO range, then the main kernel.
-hipError_t launch_bwd_pre_d64(const float *o, const float *d_o, void *workspace, int n_heads,
-                              int seq_len, hipStream_t stream);
-hipError_t launch_bwd_main_d64(const float *q, const float *k, const float *v, const float *d_o,
-                               const float *lse, float *d_q, float *d_k, float *d_v,
-                               const void *workspace, int n_heads, int seq_len, float scale,
-                               bool causal, hipStream_t stream);
+// The two phases of launch_bwd_d64: the workspace (Delta, the dO range and
+// the fp16 operand copies), then the main kernel, which reads only the
+// workspace, lse and its outputs.
+hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
+                              const float *d_o, void *workspace, int n_heads, int seq_len, float scale,
+                              hipStream_t stream);
+hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
+                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream);
 
 // Generic fp32 kernels for any d_head in 1..=128 and any 4-byte alignment.
 // The backward recomputes everything it needs per row and uses no workspace.

@@ -18,8 +18,8 @@
  *
  *  2. The fast path, which the reference does not have: a forward that also
  *     writes the natural-log logsumexp of every query row, and a backward that
- *     recomputes P from that logsumexp with an O(H*S) workspace instead of the
- *     reference's H*2*S*S probability scratch. These take an explicit HIP
+ *     recomputes P from that logsumexp with an O(H*S*D) workspace instead of
+ *     the reference's H*2*S*S probability scratch. These take an explicit HIP
  *     stream and return a status code; nothing aborts.
  *
  * Tensor layout (both groups), as in attention_fused.cu:60-66 and :404-414:
@@ -108,8 +108,10 @@ int dfattn_fwd(const float *q, const float *k, const float *v, float *o,
                float *lse, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                float scale, uint32_t causal, void *stream);
 
-/* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len)
- * (row statistics Delta_i = dO_i . O_i and a per-head dO range scale).
+/* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len * d_head)
+ * (row statistics Delta_i = dO_i . O_i, a per-head dO range scale, and fp16
+ * copies of the scaled Q, K, V and dO that the main phase reads; 8 bytes
+ * per element of one input, 25 MB at H = 12, S = 4096, D = 64).
  * Returns 0 when the arguments are invalid.                                */
 size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len,
                                   uint32_t d_head);
@@ -126,16 +128,19 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o,
 
 /* The two phases of dfattn_bwd, for callers that schedule or time them
  * separately (dfattn_bwd is exactly preprocess then main, on one stream,
- * with one workspace). Preprocess reads O and dO and writes the workspace's
- * row statistics; main reads them and writes dQ, dK, dV. No reference
- * counterpart: the reference backward is one kernel without saved
- * statistics (attention_fused.cu:390-516).                                  */
-int dfattn_bwd_preprocess(const float *o, const float *d_o, void *workspace,
+ * with one workspace). Preprocess reads Q, K, V, O and dO and fills the
+ * workspace (row statistics and the fp16 operand copies); main reads the
+ * workspace and lse and writes dQ, dK, dV. Pass both phases the same
+ * q, k, v, o, d_o, workspace and scale. No reference counterpart: the
+ * reference backward is one kernel without saved statistics
+ * (attention_fused.cu:390-516).                                             */
+int dfattn_bwd_preprocess(const float *q, const float *k, const float *v,
+                          const float *o, const float *d_o, void *workspace,
                           size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
-                          uint32_t d_head, void *stream);
+                          uint32_t d_head, float scale, void *stream);
 int dfattn_bwd_main(const float *q, const float *k, const float *v,
-                    const float *d_o, const float *lse, float *d_q, float *d_k,
-                    float *d_v, void *workspace, size_t workspace_bytes,
+                    const float *o, const float *d_o, const float *lse, float *d_q,
+                    float *d_k, float *d_v, void *workspace, size_t workspace_bytes,
                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                     float scale, uint32_t causal, void *stream);
 
@@ -143,7 +148,7 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v,
  * Mirror of AttentionContext (darkforest-cuda/src/lib.rs:1949-2368), the
  * object each layer of the reference's static GPT-2 engine owns
  * (static_gpt2.rs:401-406). All device buffers it needs (logsumexp [H, S]
- * and the backward workspace, O(H*S)) are allocated by create; the reference
+ * and the backward workspace, O(H*S*D)) are allocated by create; the reference
  * instead allocates an H*2*S*S scratch on the first backward (lib.rs:2019).
  * The context is internally locked, like the reference's Mutex fields.    */
 typedef struct dfattn_context dfattn_context;

@@ -315,3 +315,32 @@ def test_forward_is_deterministic_and_stream_ordered(device):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+def test_split_backward_phases_match_dfattn_bwd(device):
+    """dfattn_bwd_preprocess + dfattn_bwd_main give dfattn_bwd's gradients bit for bit, also when
+    one of q, k, v, o, d_o is only 4-byte aligned (then both phases take the generic path)."""
+    import torch
+
+    say("split backward phases")
+    x = O.seeded_inputs(384, 12, 64, 3300)
+    q, k, v, g = (to_dev(x[n], device) for n in ("q", "k", "v", "do"))
+    o, lse = dfattn.attention_forward(q, k, v, 12, 0.125, True)
+    ref = dfattn.attention_backward(q, k, v, o, g, lse, 12, 0.125, True)
+    ws = torch.empty(dfattn.bwd_workspace_bytes(12, 384, 64) // 4, device=device)
+    got = [torch.empty_like(q) for _ in range(3)]
+    dfattn.backward_preprocess(q, k, v, o, g, ws, 12, 0.125)
+    dfattn.backward_main(q, k, v, o, g, lse, *got, ws, 12, 0.125, True)
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    # o moved by one float: 4-byte aligned only.
+    buf = torch.empty(o.numel() + 1, device=device)
+    o4 = buf[1:].view_as(o)
+    o4.copy_(o)
+    ws.fill_(float("nan"))
+    dfattn.backward_preprocess(q, k, v, o4, g, ws, 12, 0.125)
+    dfattn.backward_main(q, k, v, o4, g, lse, *got, ws, 12, 0.125, True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert_close(f"split, unaligned o, {name}", host(a), host(b), scaled=True)
