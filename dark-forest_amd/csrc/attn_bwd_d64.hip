@@ -407,6 +407,9 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
       s = mfma32x32x16(qa[ds], kf[ds], s);
       dp = mfma32x32x16(ga[ds], vf[ds], dp);
     }
+    // The transposed reads start after the products that consume qa and ga,
+    // so their registers are free again (the exp of S hides the reads).
+    __builtin_amdgcn_sched_barrier(0);
     // dO^T and (c2 Q)^T slots for this wave's two query steps.
     half8_t gtr[2][2], qtr[2][2];
 #pragma unroll
@@ -693,9 +696,12 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 
   auto iter = [&](int t, auto u) {
     constexpr int q = decltype(u)::value;
-    compute(t, q, false);
+    // Tile t+3 goes into its stage (last read in iteration t-1) and tile t+5
+    // is fetched before the products of tile t, so the fetch has most of
+    // three iterations to arrive.
     store_tile((q + 3) & 3, Const<(q + 3) & 1>{});
     load_tile(t + 5, Const<(q + 3) & 1>{});
+    compute(t, q, false);
     __syncthreads();
   };
   int t = 0;
@@ -706,7 +712,6 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     iter(t + 3, Const<3>{});
   }
   for (; t < n_tiles; ++t) {
-    compute(t, t & 3, true);
     if (t + 3 < n_tiles) {
       if ((t + 3) & 1) {
         store_tile((t + 3) & 3, Const<1>{});
@@ -716,6 +721,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
         if (t + 5 < n_tiles) load_tile(t + 5, Const<0>{});
       }
     }
+    compute(t, t & 3, true);
     __syncthreads();
   }
 
