@@ -272,7 +272,7 @@ def main():
         dfattn.attention_forward(q, k, v, H, SCALE, True, out=o, lse=lse)
         if ev is not None:
             ev[1].record(stream)
-        dfattn.backward_preprocess(q, k, v, o, g, ws, H, SCALE)
+        dfattn.backward_preprocess(q, k, v, o, g, lse, ws, H, SCALE)
         if ev is not None:
             ev[2].record(stream)
         dfattn.backward_main(q, k, v, o, g, lse, dq, dk, dv, ws, H, SCALE, True)

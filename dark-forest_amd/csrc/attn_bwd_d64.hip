@@ -125,17 +125,21 @@ template <int N>
 using Const = std::integral_constant<int, N>;
 
 // Workspace layout (bytes): Delta [H*S] fp32 | dO block max [H*ceil(S/64)]
-// fp32 | then, 256-byte aligned, the fp16 copies c2*Q, K, V and sigma*dO,
-// each [H][S][64].
+// fp32 | then, 256-byte aligned, the row statistics as the main kernel's
+// products take them, -lse*log2(e) and -Delta*sigma, each [H][S] fp32, and
+// the fp16 copies c2*Q, K, V and sigma*dO, each [H][S][64].
 struct WsLayout {
-  size_t blockmax, q16, k16, v16, do16, total;
+  size_t blockmax, lse2n, deltan, q16, k16, v16, do16, total;
 };
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 inline WsLayout ws_layout(int H, int S) {
   WsLayout w;
   w.blockmax = ws_delta_floats(H, S) * sizeof(float);
+  const size_t stat = align256((size_t)H * S * sizeof(float));
   const size_t copy = align256((size_t)H * S * kD * sizeof(half_t));
-  w.q16 = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
+  w.lse2n = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
+  w.deltan = w.lse2n + stat;
+  w.q16 = w.deltan + stat;
   w.k16 = w.q16 + copy;
   w.v16 = w.k16 + copy;
   w.do16 = w.v16 + copy;
@@ -143,17 +147,18 @@ inline WsLayout ws_layout(int H, int S) {
   return w;
 }
 
-// fp16 copies for the main kernel: 64 rows of one head per workgroup (256
-// threads; thread t converts row t/4, columns 16*(t%4) .. +15 of each
-// tensor). c2*Q is rounded as the forward rounds its Q (round_scaled4);
+// fp16 copies and row statistics for the main kernel: 64 rows of one head
+// per workgroup (256 threads; thread t converts row t/4, columns
+// 16*(t%4) .. +15 of each tensor). c2*Q is rounded as the forward rounds its Q (round_scaled4);
 // sigma is the head's power of two from the preprocess block maxima, so
 // sigma*dO is exact in fp32 and rounds as the preprocess rounded it for
 // Delta wherever sigma*dO is an fp16 normal number.
 __global__ __launch_bounds__(256) void bwd_convert_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
-    const float *__restrict__ dO, const float *__restrict__ blockmax, half_t *__restrict__ q16,
-    half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16, int H, int S,
-    int n_pre_blocks, float c2) {
+    const float *__restrict__ dO, const float *__restrict__ lse, const float *__restrict__ delta,
+    const float *__restrict__ blockmax, float *__restrict__ lse2n, float *__restrict__ deltan,
+    half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
+    int H, int S, int n_pre_blocks, float c2) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int head = blockIdx.y;
   const int row = blockIdx.x * 64 + (tid >> 2);
@@ -172,6 +177,11 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
   for (int i = lane; i < n_pre_blocks; i += 64) gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
   const float sigma = pow2_scale(wave_max(gmax));
   if (!ok) return;
+  if ((tid & 3) == 0) {
+    const size_t r = (size_t)head * S + row;
+    lse2n[r] = -lse[r] * kLog2e;
+    deltan[r] = -(delta[r] * sigma);
+  }
   half_t *out[4] = {q16, k16, v16, do16};
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -204,7 +214,7 @@ constexpr int kCostQStep = 25;
 // scale).
 struct BwdArgs {
   const half_t *Q16, *K16, *V16, *dO16;
-  const float *LSE, *delta, *blockmax;
+  const float *lse2n, *deltan, *blockmax;
   float *dQ, *dK, *dV;
   int H, S, causal, n_pre_blocks;
   float scale;
@@ -230,11 +240,6 @@ template <int NRows>
 __device__ __forceinline__ auto rows16_rsrc(const half_t *p, int head, int S, int row0) {
   const unsigned nrec = (unsigned)max(0, min(S - row0, NRows)) * kD * 2;
   return buffer_rsrc(p + ((size_t)head * S + min(row0, S)) * kD, nrec);
-}
-// This thread's granule of the 64 rows from row0.
-__device__ __forceinline__ half8_t load_granule16(const half_t *p, int head, int S, int row0) {
-  const auto rs = rows16_rsrc<64>(p, head, S, row0);
-  return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs, threadIdx.x * 16, 0, 0));
 }
 // This thread's two granules of the 128 rows from row0.
 __device__ __forceinline__ void load_rows16(const half_t *p, int head, int S, int row0, half8_t (&g)[kOwnG]) {
@@ -333,46 +338,37 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         troff[j][db][hf] = tile_tr4_off(16 * (2 * qh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-  const int soff = tile_off(tid >> 3, (tid & 7) * 8);  // this thread's granule of a staged tile
-
+  // Direct-to-LDS staging of query block i (its c2*Q and sigma*dO rows and
+  // its two row statistics) into ring stage st: wave w fetches rows 8w ..
+  // 8w+7 of each tile (1 KB; lane l's 16 bytes land at byte 16*l of the
+  // wave's kilobyte, so it fetches the global granule the swizzle places
+  // there); waves 0 and 1 also fetch the 64 values of -lse*log2(e) and
+  // -Delta*sigma. Rows past S read as zeros (they then contribute nothing:
+  // their Q and dO rows are zero too).
   auto stage_base = [&](int st) { return lds_raw + st * kStageBytes; };
-  // Staged rows of c2*Q and sigma*dO (one granule per thread; rows past S
-  // read as zeros) and the block's lse and Delta (lane = row; every wave
-  // loads and stores the same 64 values).
-  half8_t qreg[2], greg[2];
-  float lraw[2], draw[2];
-  auto load_regs = [&](int i, half8_t &qr, half8_t &gr, float &lr, float &dr) {
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int drow = 8 * wave + (lane >> 3);
+  const int dma_off = drow * 128 + (((lane & 7) ^ tile_swz(drow)) << 4);
+  auto dma_block = [&](int i, int st) {
     const int qb0 = (first_qb + i) * kQBlock;
-    qr = load_granule16(a.Q16, head, S, qb0);
-    gr = load_granule16(a.dO16, head, S, qb0);
-    const unsigned srec = (unsigned)max(0, min(S - qb0, kQBlock)) * 4;
-    const size_t sbase = (size_t)head * S + min(qb0, S);
-    const auto rl = buffer_rsrc(a.LSE + sbase, srec);
-    const auto rd = buffer_rsrc(a.delta + sbase, srec);
-    lr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, lane * 4, 0, 0));
-    dr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, lane * 4, 0, 0));
+    const int rows = max(0, min(S - qb0, kQBlock));
+    const size_t base = (size_t)head * S + min(qb0, S);
+    const unsigned qt = lds_addr32(stage_base(st) + wave * 1024);
+    lds_fetch16(sgpr_rsrc(a.Q16 + base * kD, (unsigned)rows * kD * 2), qt, dma_off);
+    lds_fetch16(sgpr_rsrc(a.dO16 + base * kD, (unsigned)rows * kD * 2), qt + kTile * 2, dma_off);
+    if (wave_u < 2)
+      lds_fetch4(sgpr_rsrc((wave_u == 0 ? a.lse2n : a.deltan) + base, (unsigned)rows * 4),
+                 lds_addr32(stage_base(st) + 2 * kTile * 2 + wave_u * kQBlock * 4), lane * 4);
   };
-  // The statistics are stored negated (they enter the products as
-  // accumulator inputs), rows past S get lse = +inf so that P = 0.
+  // Barrier after block i+1 has landed, with the fetches of blocks i+2 and
+  // i+3 (two per block, three for waves 0 and 1) still in flight.
+  auto fetch_barrier = [&]() {
+    if (wave_u < 2)
+      lds_fetch_barrier<6>();
+    else
+      lds_fetch_barrier<4>();
+  };
   float sigma = 1.f;
-  auto store_regs = [&](int i, int st, const half8_t &qr, const half8_t &gr, float lr, float dr) {
-    half_t *qt = reinterpret_cast<half_t *>(stage_base(st));
-    half_t *gt = qt + kTile;
-    float *sl = reinterpret_cast<float *>(gt + kTile);
-    *reinterpret_cast<half8_t *>(qt + soff) = qr;
-    *reinterpret_cast<half8_t *>(gt + soff) = gr;
-    const int row = (first_qb + i) * kQBlock + lane;
-    sl[lane] = row < S ? -lr * kLog2e : -INFINITY;
-    sl[kQBlock + lane] = -(dr * sigma);
-  };
-  auto load_block = [&](int i, auto set) {
-    constexpr int b = decltype(set)::value;
-    load_regs(i, qreg[b], greg[b], lraw[b], draw[b]);
-  };
-  auto store_block = [&](int i, int st, auto set) {
-    constexpr int b = decltype(set)::value;
-    store_regs(i, st, qreg[b], greg[b], lraw[b], draw[b]);
-  };
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
@@ -445,40 +441,26 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     }
   };
 
-  // Generic iteration (head and remainder): runtime stage and register set.
+  // Generic iteration (head and remainder): runtime stage; waits for every
+  // fetch at its end.
   auto step = [&](int i, bool masked) {
+    if (i + 3 < nb) dma_block(i + 3, (i + 3 - i0) & 3);
     compute(i, (i - i0) & 3, masked);
-    if (i + 3 < nb) {
-      if ((i + 3) & 1) {
-        store_block(i + 3, (i + 3 - i0) & 3, Const<1>{});
-        if (i + 5 < nb) load_block(i + 5, Const<1>{});
-      } else {
-        store_block(i + 3, (i + 3 - i0) & 3, Const<0>{});
-        if (i + 5 < nb) load_block(i + 5, Const<0>{});
-      }
-    }
-    __syncthreads();
+    lds_fetch_barrier<0>();
   };
 
-  // Prologue: every load is issued before the first wait (blocks 0-2 into
-  // prologue registers, blocks 3 and 4 into their sets; loads past the end
-  // read zeros into stages that are never read), then sigma, then blocks 0-2
-  // go into the ring.
-  {
-    half8_t qp[3], gp[3];
-    float lp[3], dpr[3];
+  // Prologue: blocks 0-2 are fetched into their stages, the workgroup's K
+  // and V rows go through registers into LDS, then every fetch is awaited.
 #pragma unroll
-    for (int p = 0; p < 3; ++p) load_regs(p, qp[p], gp[p], lp[p], dpr[p]);
-    load_block(3, Const<1>{});
-    load_block(4, Const<0>{});
-    sigma = head_sigma(bmax);
+  for (int p = 0; p < 3; ++p)
+    if (p < nb) dma_block(p, (p - i0) & 3);
+  sigma = head_sigma(bmax);
+  {
     half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
     store_rows16(own, kown);
     store_rows16(own + kOwnTile, vown);
-#pragma unroll
-    for (int p = 0; p < 3; ++p) store_regs(p, (p - i0) & 3, qp[p], gp[p], lp[p], dpr[p]);
   }
-  __syncthreads();
+  lds_fetch_barrier<0>();
   {
     // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
     // holds key key0 + c, slots d = 16*ds + 8*hh + j.
@@ -496,10 +478,9 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // (i - i0 is a multiple of 4 at the top of each trip).
   auto iter = [&](int ii, auto u) {
     constexpr int q = decltype(u)::value;
+    dma_block(ii + 3, (q + 3) & 3);
     compute(ii, q, false);
-    store_block(ii + 3, (q + 3) & 3, Const<(q + 3) & 1>{});
-    load_block(ii + 5, Const<(q + 3) & 1>{});
-    __syncthreads();
+    fetch_barrier();
   };
   for (; i + 4 <= nb; i += 4) {
     iter(i, Const<0>{});
@@ -508,6 +489,9 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     iter(i + 3, Const<3>{});
   }
   for (; i < nb; ++i) step(i, false);
+  // Fetches of blocks past the end may still be landing in the ring, which
+  // the exchange below reuses.
+  lds_fetch_barrier<0>();
 
   // Wave w finishes dK and wave w+4 dV of the same 32 keys.
   float *buf = reinterpret_cast<float *>(lds_raw);
@@ -558,8 +542,9 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   half8_t qown[kOwnG], gown[kOwnG];
   load_rows16(a.Q16, head, S, q_blk0, qown);
   load_rows16(a.dO16, head, S, q_blk0, gown);
-  const float Lraw = q_ok ? a.LSE[(size_t)head * S + query] : 0.f;
-  const float Draw = q_ok ? a.delta[(size_t)head * S + query] : 0.f;
+  // The lane's -lse*log2(e) and -Delta*sigma (rows past S: P = 0).
+  const float nl = q_ok ? a.lse2n[(size_t)head * S + query] : -INFINITY;
+  const float nd = q_ok ? a.deltan[(size_t)head * S + query] : 0.f;
   half8_t qf[4], gf[4];
   f32x16 negL, negD;
   float sigma;
@@ -584,30 +569,22 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         ktoff[j][db][hf] = tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-  const int soff = tile_off(tid >> 3, (tid & 7) * 8);  // this thread's granule of a staged tile
-
-  // Tile t goes through ring stage t % 4 and register set t % 2; tile t+3
-  // is written during iteration t (into the stage last read in iteration
-  // t-1) and tile t+5 is fetched into the set tile t+3 has just left. Keys
-  // past S read as zeros and are masked to P = 0.
+  // Tile t goes through ring stage t % 4; tile t+3 is fetched at the start
+  // of iteration t (into the stage last read in iteration t-1). Keys past S
+  // read as zeros and are masked to P = 0.
   auto stage_base = [&](int st) { return reinterpret_cast<half_t *>(lds_raw + st * kStageBytes); };
-  half8_t kreg[2], vreg[2];
-  auto load_regs = [&](int t, half8_t &kr, half8_t &vr) {
-    kr = load_granule16(a.K16, head, S, t * kKTile);
-    vr = load_granule16(a.V16, head, S, t * kKTile);
-  };
-  auto store_regs = [&](int st, const half8_t &kr, const half8_t &vr) {
-    half_t *kt = stage_base(st);
-    *reinterpret_cast<half8_t *>(kt + soff) = kr;
-    *reinterpret_cast<half8_t *>(kt + kTile + soff) = vr;
-  };
-  auto load_tile = [&](int t, auto set) {
-    constexpr int b = decltype(set)::value;
-    load_regs(t, kreg[b], vreg[b]);
-  };
-  auto store_tile = [&](int st, auto set) {
-    constexpr int b = decltype(set)::value;
-    store_regs(st, kreg[b], vreg[b]);
+  // Direct-to-LDS: wave w fetches rows 8w .. 8w+7 of each K and V tile (1 KB
+  // each); lane l's 16 bytes land at byte 16*l of the wave's kilobyte, so
+  // it fetches the global granule the swizzle places there.
+  const int drow = 8 * wave + (lane >> 3);
+  const int dma_off = drow * 128 + (((lane & 7) ^ tile_swz(drow)) << 4);
+  auto dma_tile = [&](int t, int st) {
+    const unsigned kt = lds_addr32(lds_raw + st * kStageBytes + wave * 1024);
+    const int row0 = t * kKTile;
+    const unsigned nrec = (unsigned)max(0, min(S - row0, kKTile)) * kD * 2;
+    const size_t base = ((size_t)head * S + min(row0, S)) * kD;
+    lds_fetch16(sgpr_rsrc(a.K16 + base, nrec), kt, dma_off);
+    lds_fetch16(sgpr_rsrc(a.V16 + base, nrec), kt + kTile * 2, dma_off);
   };
 
   f32x16 dq[2];
@@ -663,26 +640,20 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // prologue registers, tiles 3 and 4 into their sets), then sigma and the
   // fragments, then tiles 0-2 go into the ring.
   {
-    half8_t kp[3], vp[3];
 #pragma unroll
-    for (int p = 0; p < 3; ++p) load_regs(p, kp[p], vp[p]);
-    load_tile(3, Const<1>{});
-    load_tile(4, Const<0>{});
+    for (int p = 0; p < 3; ++p)
+      if (p < n_tiles) dma_tile(p, p);
     sigma = head_sigma(bmax);
     half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
     store_rows16(own, qown);
     store_rows16(own + kOwnTile, gown);
-    const float L = q_ok ? Lraw * kLog2e : INFINITY;
-    const float Dl = Draw * sigma;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      negL[r] = -L;
-      negD[r] = -Dl;
+      negL[r] = nl;
+      negD[r] = nd;
     }
-#pragma unroll
-    for (int p = 0; p < 3; ++p) store_regs(p & 3, kp[p], vp[p]);
   }
-  __syncthreads();
+  lds_fetch_barrier<0>();
   {
     // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds query
     // q_w0 + c, slots d = 16*ds + 8*hh + j.
@@ -699,10 +670,9 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     // Tile t+3 goes into its stage (last read in iteration t-1) and tile t+5
     // is fetched before the products of tile t, so the fetch has most of
     // three iterations to arrive.
-    store_tile((q + 3) & 3, Const<(q + 3) & 1>{});
-    load_tile(t + 5, Const<(q + 3) & 1>{});
+    dma_tile(t + 3, (q + 3) & 3);
     compute(t, q, false);
-    __syncthreads();
+    lds_fetch_barrier<4>();  // tile t+1 has landed; tiles t+2, t+3 may be in flight
   };
   int t = 0;
   for (; t + 4 <= n_full; t += 4) {
@@ -712,18 +682,13 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     iter(t + 3, Const<3>{});
   }
   for (; t < n_tiles; ++t) {
-    if (t + 3 < n_tiles) {
-      if ((t + 3) & 1) {
-        store_tile((t + 3) & 3, Const<1>{});
-        if (t + 5 < n_tiles) load_tile(t + 5, Const<1>{});
-      } else {
-        store_tile((t + 3) & 3, Const<0>{});
-        if (t + 5 < n_tiles) load_tile(t + 5, Const<0>{});
-      }
-    }
+    if (t + 3 < n_tiles) dma_tile(t + 3, (t + 3) & 3);
     compute(t, t & 3, true);
-    __syncthreads();
+    lds_fetch_barrier<0>();
   }
+  // Fetches of tiles past the end may still be landing in the ring, which
+  // the exchange below reuses.
+  lds_fetch_barrier<0>();
 
   // Wave w finishes columns 0-31 of dQ and wave w+4 columns 32-63 of the
   // same 32 rows (each gives up the other block).
@@ -817,8 +782,8 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) { return ws_layout(n_heads, seq_len).total; }
 
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
-                              const float *d_o, void *workspace, int n_heads, int seq_len, float scale,
-                              hipStream_t stream) {
+                              const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
+                              float scale, hipStream_t stream) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   float *delta = reinterpret_cast<float *>(ws);
@@ -827,9 +792,11 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      o, d_o, delta, blockmax, n_heads, seq_len);
   if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
   hipLaunchKernelGGL(bwd_convert_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v,
-                     d_o, blockmax, reinterpret_cast<half_t *>(ws + w.q16), reinterpret_cast<half_t *>(ws + w.k16),
-                     reinterpret_cast<half_t *>(ws + w.v16), reinterpret_cast<half_t *>(ws + w.do16), n_heads,
-                     seq_len, pre_blocks(seq_len), scale * kLog2e);
+                     d_o, lse, delta, blockmax, reinterpret_cast<float *>(ws + w.lse2n),
+                     reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
+                     reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
+                     reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, pre_blocks(seq_len),
+                     scale * kLog2e);
   return hipGetLastError();
 }
 
@@ -842,8 +809,8 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
   a.K16 = reinterpret_cast<const half_t *>(ws + w.k16);
   a.V16 = reinterpret_cast<const half_t *>(ws + w.v16);
   a.dO16 = reinterpret_cast<const half_t *>(ws + w.do16);
-  a.LSE = lse;
-  a.delta = reinterpret_cast<const float *>(ws);
+  a.lse2n = reinterpret_cast<const float *>(ws + w.lse2n);
+  a.deltan = reinterpret_cast<const float *>(ws + w.deltan);
   a.blockmax = reinterpret_cast<const float *>(ws + w.blockmax);
   a.dQ = d_q;
   a.dK = d_k;
@@ -880,7 +847,7 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
                           bool causal, hipStream_t stream) {
-  hipError_t err = launch_bwd_pre_d64(q, k, v, o, d_o, workspace, n_heads, seq_len, scale, stream);
+  hipError_t err = launch_bwd_pre_d64(q, k, v, o, d_o, lse, workspace, n_heads, seq_len, scale, stream);
   if (err != hipSuccess) return err;
   return launch_bwd_main_d64(lse, d_q, d_k, d_v, workspace, n_heads, seq_len, scale, causal, stream);
 }

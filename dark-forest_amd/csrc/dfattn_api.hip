@@ -244,17 +244,17 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o, c
 // The split backward decides the fast path from q, k, v, o and d_o in both
 // phases, so main takes it only when preprocess filled the workspace.
 int dfattn_bwd_preprocess(const float *q, const float *k, const float *v, const float *o,
-                          const float *d_o, void *workspace, size_t workspace_bytes,
+                          const float *d_o, const float *lse, void *workspace, size_t workspace_bytes,
                           uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale,
                           void *stream) {
   const char *fn = "dfattn_bwd_preprocess";
   int st = check_shape(fn, n_heads, seq_len, d_head);
-  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o});
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse});
   if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
   if (st != DFATTN_OK) return st;
   // The generic kernel recomputes its row statistics itself: nothing to do.
   if (!fast_path(d_head, {q, k, v, o, d_o})) return DFATTN_OK;
-  return record_hip(dfattn::launch_bwd_pre_d64(q, k, v, o, d_o, workspace, (int)n_heads, (int)seq_len,
+  return record_hip(dfattn::launch_bwd_pre_d64(q, k, v, o, d_o, lse, workspace, (int)n_heads, (int)seq_len,
                                                scale, static_cast<hipStream_t>(stream)),
                     "attention backward preprocess launch");
 }

@@ -21,6 +21,55 @@ constexpr float kLog2e = 1.4426950408889634f;
 // swizzle); loads past num_records return zeros.
 constexpr int kBufferFlags = 0x00020000;
 
+// Direct-to-LDS fetch: 16 bytes per lane from the buffer (descriptor in
+// scalar registers, see sgpr_rsrc) at byte offset voff into LDS at
+// lds_addr + 16 * lane (lds_addr uniform across the wave). The data bypasses
+// the registers; the wave's vmcnt counts the fetch until it has landed in
+// LDS. The instruction is issued through asm so that the compiler does not
+// see an LDS write: it would otherwise wait for every fetch in flight before
+// the next LDS read it cannot prove disjoint (the transposing reads), which
+// defeats the prefetch. The caller synchronises with lds_fetch_barrier; the
+// compiler's own vmcnt waits for its loads can only over-count these.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 sgpr_rsrc(const void *p, unsigned nrec) {
+  const unsigned long long addr = reinterpret_cast<unsigned long long>(p);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(unsigned)addr);
+  r.y = __builtin_amdgcn_readfirstlane((int)((unsigned)(addr >> 32) & 0xffffu));
+  r.z = __builtin_amdgcn_readfirstlane((int)nrec);
+  r.w = kBufferFlags;
+  return r;
+}
+// LDS address of p as a wave-uniform 32-bit value (the caller guarantees
+// uniformity across the wave; readfirstlane puts it in a scalar register).
+__device__ __forceinline__ unsigned lds_addr32(const unsigned char *p) {
+  return __builtin_amdgcn_readfirstlane(
+      (unsigned)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) unsigned char *)p));
+}
+// M0 is reserved to the compiler, which warns that it is not restored after
+// the asm; these kernels use M0 for nothing else.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_fetch16(i32x4 rsrc, unsigned lds_addr, int voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr), "s"(rsrc)
+               : "memory", "m0");
+}
+// The same for 4 bytes per lane (LDS at lds_addr + 4 * lane).
+__device__ __forceinline__ void lds_fetch4(i32x4 rsrc, unsigned lds_addr, int voff) {
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(voff), "s"(lds_addr), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Workgroup barrier after this wave's LDS writes and all but its N most
+// recent vector-memory operations have completed: with direct-to-LDS
+// fetches in flight, N of them (the prefetches of later tiles) may stay
+// outstanding across the barrier. The compiler's own barrier waits for
+// every vector-memory operation.
+template <int N>
+__device__ __forceinline__ void lds_fetch_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Raw buffer descriptor over nrec bytes from p. The kernels build descriptors
 // only from workgroup-uniform values; readfirstlane states that, which keeps
 // the descriptor in scalar registers (a clamp the compiler lowers to a vector
@@ -204,8 +253,8 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
 // the fp16 operand copies), then the main kernel, which reads only the
 // workspace, lse and its outputs.
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
-                              const float *d_o, void *workspace, int n_heads, int seq_len, float scale,
-                              hipStream_t stream);
+                              const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
+                              float scale, hipStream_t stream);
 hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
                                int n_heads, int seq_len, float scale, bool causal, hipStream_t stream);
 

@@ -49,7 +49,7 @@ SYMBOLS = {
     "dfattn_fwd": (ctypes.c_int, [_P] * 5 + [_U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
     "dfattn_bwd": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
-    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _P]),
+    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dfattn_last_error": (ctypes.c_int, []),
@@ -180,20 +180,20 @@ def attention_backward(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d
     return d_q, d_k, d_v
 
 
-def backward_preprocess(q, k, v, o, d_o, workspace, n_heads, scale=None, stream=None):
-    """First phase of attention_backward (row statistics Delta, the dO range and the fp16
-    operand copies, all in the workspace)."""
+def backward_preprocess(q, k, v, o, d_o, lse, workspace, n_heads, scale=None, stream=None):
+    """First phase of attention_backward (row statistics, the dO range and the fp16 operand
+    copies, all in the workspace)."""
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5
     _check(lib().dfattn_bwd_preprocess(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o),
-                                       _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
+                                       _dev_ptr(lse), _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
                                        n_heads, seq_len, d_head, scale, _stream_ptr(stream)))
 
 
 def backward_main(q, k, v, o, d_o, lse, d_q, d_k, d_v, workspace, n_heads, scale=None, causal=True, stream=None):
     """Second phase of attention_backward (the fused dQ/dK/dV kernel); same q, k, v, o, d_o,
-    workspace and scale as backward_preprocess."""
+    lse, workspace and scale as backward_preprocess."""
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5

@@ -109,9 +109,10 @@ int dfattn_fwd(const float *q, const float *k, const float *v, float *o,
                float scale, uint32_t causal, void *stream);
 
 /* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len * d_head)
- * (row statistics Delta_i = dO_i . O_i, a per-head dO range scale, and fp16
- * copies of the scaled Q, K, V and dO that the main phase reads; 8 bytes
- * per element of one input, 25 MB at H = 12, S = 4096, D = 64).
+ * (row statistics Delta_i = dO_i . O_i, a per-head dO range scale, the row
+ * statistics as the main phase's products take them, and fp16 copies of the
+ * scaled Q, K, V and dO that the main phase reads; 8 bytes per element of
+ * one input, 25 MB at H = 12, S = 4096, D = 64).
  * Returns 0 when the arguments are invalid.                                */
 size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len,
                                   uint32_t d_head);
@@ -128,16 +129,16 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o,
 
 /* The two phases of dfattn_bwd, for callers that schedule or time them
  * separately (dfattn_bwd is exactly preprocess then main, on one stream,
- * with one workspace). Preprocess reads Q, K, V, O and dO and fills the
- * workspace (row statistics and the fp16 operand copies); main reads the
- * workspace and lse and writes dQ, dK, dV. Pass both phases the same
- * q, k, v, o, d_o, workspace and scale. No reference counterpart: the
+ * with one workspace). Preprocess reads Q, K, V, O, dO and lse and fills
+ * the workspace (row statistics and the fp16 operand copies); main reads
+ * the workspace and writes dQ, dK, dV. Pass both phases the same
+ * q, k, v, o, d_o, lse, workspace and scale. No reference counterpart: the
  * reference backward is one kernel without saved statistics
  * (attention_fused.cu:390-516).                                             */
 int dfattn_bwd_preprocess(const float *q, const float *k, const float *v,
-                          const float *o, const float *d_o, void *workspace,
-                          size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
-                          uint32_t d_head, float scale, void *stream);
+                          const float *o, const float *d_o, const float *lse,
+                          void *workspace, size_t workspace_bytes, uint32_t n_heads,
+                          uint32_t seq_len, uint32_t d_head, float scale, void *stream);
 int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     const float *o, const float *d_o, const float *lse, float *d_q,
                     float *d_k, float *d_v, void *workspace, size_t workspace_bytes,

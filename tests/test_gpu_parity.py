@@ -329,7 +329,7 @@ def test_split_backward_phases_match_dfattn_bwd(device):
     ref = dfattn.attention_backward(q, k, v, o, g, lse, 12, 0.125, True)
     ws = torch.empty(dfattn.bwd_workspace_bytes(12, 384, 64) // 4, device=device)
     got = [torch.empty_like(q) for _ in range(3)]
-    dfattn.backward_preprocess(q, k, v, o, g, ws, 12, 0.125)
+    dfattn.backward_preprocess(q, k, v, o, g, lse, ws, 12, 0.125)
     dfattn.backward_main(q, k, v, o, g, lse, *got, ws, 12, 0.125, True)
     torch.cuda.synchronize()
     for a, b in zip(got, ref):
@@ -339,7 +339,7 @@ def test_split_backward_phases_match_dfattn_bwd(device):
     o4 = buf[1:].view_as(o)
     o4.copy_(o)
     ws.fill_(float("nan"))
-    dfattn.backward_preprocess(q, k, v, o4, g, ws, 12, 0.125)
+    dfattn.backward_preprocess(q, k, v, o4, g, lse, ws, 12, 0.125)
     dfattn.backward_main(q, k, v, o4, g, lse, *got, ws, 12, 0.125, True)
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv"), got, ref):
