@@ -118,18 +118,22 @@ constexpr int kMergeBytes = 8 * 32 * 64 * 4;
 // coalesced loads; each wave reads its register fragments from there.
 constexpr int kOwnTile = 128 * kD;  // halves
 constexpr int kOwnBytes = 2 * kOwnTile * 2;
-constexpr int kOwnG = 128 * kD / 8 / kThreads;  // granules per thread per own tile
-constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes;
+// Last, the dQ workgroup's 128 values of -lse*log2(e) and of -Delta*sigma.
+constexpr int kRowStatBytes = 2 * 128 * 4;
+constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes + kRowStatBytes;
+constexpr int kOwnOffset = kLdsBytes - kRowStatBytes - kOwnBytes;
+constexpr int kRowStatOffset = kLdsBytes - kRowStatBytes;
 
 template <int N>
 using Const = std::integral_constant<int, N>;
 
 // Workspace layout (bytes): Delta [H*S] fp32 | dO block max [H*ceil(S/64)]
-// fp32 | then, 256-byte aligned, the row statistics as the main kernel's
-// products take them, -lse*log2(e) and -Delta*sigma, each [H][S] fp32, and
-// the fp16 copies c2*Q, K, V and sigma*dO, each [H][S][64].
+// fp32 | then, 256-byte aligned, sigma of every head [H] fp32, the row
+// statistics as the main kernel's products take them, -lse*log2(e) and
+// -Delta*sigma, each [H][S] fp32, and the fp16 copies c2*Q, K, V and
+// sigma*dO, each [H][S][64].
 struct WsLayout {
-  size_t blockmax, lse2n, deltan, q16, k16, v16, do16, total;
+  size_t blockmax, sigma, lse2n, deltan, q16, k16, v16, do16, total;
 };
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 inline WsLayout ws_layout(int H, int S) {
@@ -137,7 +141,8 @@ inline WsLayout ws_layout(int H, int S) {
   w.blockmax = ws_delta_floats(H, S) * sizeof(float);
   const size_t stat = align256((size_t)H * S * sizeof(float));
   const size_t copy = align256((size_t)H * S * kD * sizeof(half_t));
-  w.lse2n = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
+  w.sigma = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
+  w.lse2n = align256(w.sigma + (size_t)H * sizeof(float));
   w.deltan = w.lse2n + stat;
   w.q16 = w.deltan + stat;
   w.k16 = w.q16 + copy;
@@ -156,7 +161,8 @@ inline WsLayout ws_layout(int H, int S) {
 __global__ __launch_bounds__(256) void bwd_convert_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     const float *__restrict__ dO, const float *__restrict__ lse, const float *__restrict__ delta,
-    const float *__restrict__ blockmax, float *__restrict__ lse2n, float *__restrict__ deltan,
+    const float *__restrict__ blockmax, float *__restrict__ sigma_out, float *__restrict__ lse2n,
+    float *__restrict__ deltan,
     half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
     int H, int S, int n_pre_blocks, float c2) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -176,6 +182,7 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
   float gmax = 0.f;
   for (int i = lane; i < n_pre_blocks; i += 64) gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
   const float sigma = pow2_scale(wave_max(gmax));
+  if (blockIdx.x == 0 && tid == 0) sigma_out[head] = sigma;
   if (!ok) return;
   if ((tid & 3) == 0) {
     const size_t r = (size_t)head * S + row;
@@ -214,48 +221,29 @@ constexpr int kCostQStep = 25;
 // scale).
 struct BwdArgs {
   const half_t *Q16, *K16, *V16, *dO16;
-  const float *lse2n, *deltan, *blockmax;
+  const float *lse2n, *deltan, *sigma;
   float *dQ, *dK, *dV;
   int H, S, causal, n_pre_blocks;
   float scale;
 };
 
-// Per-head sigma (power of two) from the preprocess block maxima of |dO|.
-// Split in two so that a workgroup's prologue can issue every global load it
-// needs before waiting on any: head_blockmax loads (the lane's share of the
-// block maxima), head_sigma reduces.
-__device__ __forceinline__ float head_blockmax(const BwdArgs &a, int head, int lane) {
-  float gmax = 0.f;
-  for (int i = lane; i < a.n_pre_blocks; i += 64)
-    gmax = fmaxf(gmax, a.blockmax[(size_t)head * a.n_pre_blocks + i]);
-  return gmax;
-}
-__device__ __forceinline__ float head_sigma(float lane_max) { return pow2_scale(wave_max(lane_max)); }
 
-// Loads from an fp16 copy ([H][S][64], 128-byte rows) through a buffer
-// descriptor that covers rows row0 .. min(row0 + n, S) - 1 of the head:
-// rows past S read as zeros. Thread t takes the 16-byte granules t, t + 512,
-// .. of the rows (row idx/8, granule idx%8), so each wave reads 1 KB runs.
-template <int NRows>
-__device__ __forceinline__ auto rows16_rsrc(const half_t *p, int head, int S, int row0) {
-  const unsigned nrec = (unsigned)max(0, min(S - row0, NRows)) * kD * 2;
-  return buffer_rsrc(p + ((size_t)head * S + min(row0, S)) * kD, nrec);
-}
-// This thread's two granules of the 128 rows from row0.
-__device__ __forceinline__ void load_rows16(const half_t *p, int head, int S, int row0, half8_t (&g)[kOwnG]) {
-  const auto rs = rows16_rsrc<128>(p, head, S, row0);
+// Direct-to-LDS fetch of rows row0 .. row0+127 of head `head` in an fp16
+// copy ([H][S][64]) into a swizzled [128][64] LDS tile: wave w fetches rows
+// 16w .. 16w+15 in two 1 KB pieces; lane l's 16 bytes land at byte 16*l of
+// a piece, so it fetches the global granule the swizzle places there. Rows
+// past S read as zeros. Two fetches per wave.
+__device__ __forceinline__ void dma_rows128(const half_t *p, int head, int S, int row0, unsigned char *tile) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned nrec = (unsigned)max(0, min(S - row0, 128)) * kD * 2;
+  const i32x4 rs = sgpr_rsrc(p + ((size_t)head * S + min(row0, S)) * kD, nrec);
 #pragma unroll
-  for (int k = 0; k < kOwnG; ++k)
-    g[k] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rs, (threadIdx.x + k * kThreads) * 16, 0, 0));
-}
-// The granules of load_rows16 into a swizzled [128][64] tile.
-__device__ __forceinline__ void store_rows16(half_t *tile, const half8_t (&g)[kOwnG]) {
-#pragma unroll
-  for (int k = 0; k < kOwnG; ++k) {
-    const int idx = threadIdx.x + k * kThreads;
-    *reinterpret_cast<half8_t *>(tile + tile_off(idx >> 3, (idx & 7) * 8)) = g[k];
+  for (int j = 0; j < 2; ++j) {
+    const int row = 16 * wave + 8 * j + (lane >> 3);
+    lds_fetch16(rs, lds_addr32(tile + (16 * wave + 8 * j) * 128), row * 128 + (((lane & 7) ^ tile_swz(row)) << 4));
   }
 }
+
 
 // Partner waves (w, w+4) hold partial sums of the same 32x32 accumulator
 // blocks. Each hands the N blocks it gives up to the other through LDS and
@@ -304,18 +292,16 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int kg = wave & 3, qh = wave >> 2;
   const int S = a.S;
   const int ld = a.H * kD, hoff = head * kD;
-  const float bmax = head_blockmax(a, head, lane);
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
   const int key = key0 + c;
+  // The head's dO scale (for the output scaling at the end).
+  const float sigma = a.sigma[head];
 
   // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
   // holds its key, slots d = 16*ds + 8*hh + j.
   // (Read from the workgroup's K/V tiles after the prologue; the rows of keys
   // kv_blk0 .. +127 are fetched with coalesced buffer loads first.)
   half8_t kf[4], vf[4];
-  half8_t kown[kOwnG], vown[kOwnG];
-  load_rows16(a.K16, head, S, kv_blk0, kown);
-  load_rows16(a.V16, head, S, kv_blk0, vown);
 
   const int n_qblocks = (S + kQBlock - 1) / kQBlock;
   const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
@@ -368,7 +354,6 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     else
       lds_fetch_barrier<4>();
   };
-  float sigma = 1.f;
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
@@ -449,22 +434,18 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     lds_fetch_barrier<0>();
   };
 
-  // Prologue: blocks 0-2 are fetched into their stages, the workgroup's K
-  // and V rows go through registers into LDS, then every fetch is awaited.
+  // Prologue: the workgroup's K and V rows and blocks 0-2 are fetched
+  // straight into LDS (blocks past the end into stages nothing reads); the
+  // first products wait for the K and V rows and block 0 only.
+  dma_rows128(a.K16, head, S, kv_blk0, lds_raw + kOwnOffset);
+  dma_rows128(a.V16, head, S, kv_blk0, lds_raw + kOwnOffset + kOwnTile * 2);
 #pragma unroll
-  for (int p = 0; p < 3; ++p)
-    if (p < nb) dma_block(p, (p - i0) & 3);
-  sigma = head_sigma(bmax);
-  {
-    half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
-    store_rows16(own, kown);
-    store_rows16(own + kOwnTile, vown);
-  }
-  lds_fetch_barrier<0>();
+  for (int p = 0; p < 3; ++p) dma_block(p, (p - i0) & 3);
+  fetch_barrier();
   {
     // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
     // holds key key0 + c, slots d = 16*ds + 8*hh + j.
-    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kOwnOffset);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
       kf[ds] = *reinterpret_cast<const half8_t *>(own + tile_off(kg * 32 + c, 8 * (2 * ds + hh)));
@@ -524,9 +505,10 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int qg = wave & 3, kh = wave >> 2;
   const int S = a.S;
   const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
-  const float bmax = head_blockmax(a, head, lane);
   const int q_w0 = q_blk0 + qg * 32;
   const int query = q_w0 + c;
+  // The head's dO scale (for the output scaling at the end).
+  const float sigma = a.sigma[head];
   const bool q_ok = query < S;
   const bool wave_active = q_w0 < S;
   const int wave_qlast = min(q_w0 + 32, S) - 1;
@@ -535,19 +517,8 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int key_lim = a.causal ? min(query, S - 1) : S - 1;
   const int key_lim_lo = a.causal ? min(q_w0, S - 1) : S - 1;
 
-  // The workgroup's c2*Q and sigma*dO rows and the lane's row statistics;
-  // the rows become the (c2 Q)^T and (sigma dO)^T fragments (B operands,
-  // lane c holds its query) through LDS, after the prologue has issued every
-  // load.
-  half8_t qown[kOwnG], gown[kOwnG];
-  load_rows16(a.Q16, head, S, q_blk0, qown);
-  load_rows16(a.dO16, head, S, q_blk0, gown);
-  // The lane's -lse*log2(e) and -Delta*sigma (rows past S: P = 0).
-  const float nl = q_ok ? a.lse2n[(size_t)head * S + query] : -INFINITY;
-  const float nd = q_ok ? a.deltan[(size_t)head * S + query] : 0.f;
   half8_t qf[4], gf[4];
   f32x16 negL, negD;
-  float sigma;
 
   const int kv_end = a.causal ? min(S, q_blk0 + kQueriesPerWg) : S;
   const int n_tiles = (kv_end + kKTile - 1) / kKTile;
@@ -636,28 +607,37 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     }
   };
 
-  // Prologue: every load is issued before the first wait (tiles 0-2 into
-  // prologue registers, tiles 3 and 4 into their sets), then sigma and the
-  // fragments, then tiles 0-2 go into the ring.
+  // Prologue: the workgroup's c2*Q and sigma*dO rows, its rows' -lse*log2(e)
+  // and -Delta*sigma (waves 0-3, 64 values each) and tiles 0-2 are fetched
+  // straight into LDS (tiles past the end into stages nothing reads); the
+  // first products wait for all but tiles 1 and 2.
+  dma_rows128(a.Q16, head, S, q_blk0, lds_raw + kOwnOffset);
+  dma_rows128(a.dO16, head, S, q_blk0, lds_raw + kOwnOffset + kOwnTile * 2);
   {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    if (wave_u < 4) {
+      const int row0 = q_blk0 + 64 * (wave_u & 1);
+      const unsigned nrec = (unsigned)max(0, min(S - row0, 64)) * 4;
+      const float *stat = (wave_u < 2 ? a.lse2n : a.deltan) + (size_t)head * S + min(row0, S);
+      lds_fetch4(sgpr_rsrc(stat, nrec), lds_addr32(lds_raw + kRowStatOffset + wave_u * 256), lane * 4);
+    }
+  }
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
-      if (p < n_tiles) dma_tile(p, p);
-    sigma = head_sigma(bmax);
-    half_t *own = reinterpret_cast<half_t *>(lds_raw + kLdsBytes - kOwnBytes);
-    store_rows16(own, qown);
-    store_rows16(own + kOwnTile, gown);
+  for (int p = 0; p < 3; ++p) dma_tile(p, p);
+  lds_fetch_barrier<4>();
+  {
+    // The lane's -lse*log2(e) and -Delta*sigma (rows past S: P = 0), and the
+    // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds query
+    // q_w0 + c, slots d = 16*ds + 8*hh + j.
+    const float *rs = reinterpret_cast<const float *>(lds_raw + kRowStatOffset);
+    const float nl = q_ok ? rs[qg * 32 + c] : -INFINITY;
+    const float nd = q_ok ? rs[128 + qg * 32 + c] : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       negL[r] = nl;
       negD[r] = nd;
     }
-  }
-  lds_fetch_barrier<0>();
-  {
-    // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds query
-    // q_w0 + c, slots d = 16*ds + 8*hh + j.
-    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kLdsBytes - kOwnBytes);
+    const half_t *own = reinterpret_cast<const half_t *>(lds_raw + kOwnOffset);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
       qf[ds] = *reinterpret_cast<const half8_t *>(own + tile_off(qg * 32 + c, 8 * (2 * ds + hh)));
@@ -792,7 +772,8 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      o, d_o, delta, blockmax, n_heads, seq_len);
   if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
   hipLaunchKernelGGL(bwd_convert_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v,
-                     d_o, lse, delta, blockmax, reinterpret_cast<float *>(ws + w.lse2n),
+                     d_o, lse, delta, blockmax, reinterpret_cast<float *>(ws + w.sigma),
+                     reinterpret_cast<float *>(ws + w.lse2n),
                      reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
                      reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
                      reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, pre_blocks(seq_len),
@@ -811,7 +792,7 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
   a.dO16 = reinterpret_cast<const half_t *>(ws + w.do16);
   a.lse2n = reinterpret_cast<const float *>(ws + w.lse2n);
   a.deltan = reinterpret_cast<const float *>(ws + w.deltan);
-  a.blockmax = reinterpret_cast<const float *>(ws + w.blockmax);
+  a.sigma = reinterpret_cast<const float *>(ws + w.sigma);
   a.dQ = d_q;
   a.dK = d_k;
   a.dV = d_v;
