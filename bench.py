@@ -269,10 +269,10 @@ def main():
     def step(ev=None):
         if ev is not None:
             ev[0].record(stream)
-        dfattn.attention_forward(q, k, v, H, SCALE, True, out=o, lse=lse)
+        dfattn.forward_train(q, k, v, H, ws, SCALE, True, out=o, lse=lse)
         if ev is not None:
             ev[1].record(stream)
-        dfattn.backward_preprocess(q, k, v, o, g, lse, ws, H, SCALE)
+        dfattn.backward_preprocess(q, k, v, o, g, lse, ws, H, SCALE, flags=dfattn.BWD_QKV_SAVED)
         if ev is not None:
             ev[2].record(stream)
         dfattn.backward_main(q, k, v, o, g, lse, dq, dk, dv, ws, H, SCALE, True)

@@ -72,10 +72,13 @@ int check_dims(uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   return DFATTN_OK;
 }
 
+// The forward also leaves the backward's fp16 copies of Q, K and V in the
+// context's workspace (dfattn_fwd_train), which the backward on the same
+// q, k, v then reuses.
 int run_forward(dfattn_context *c, const float *q, const float *k, const float *v, float scale,
                 uint32_t causal, float *out, void *stream) {
-  const int st = dfattn_fwd(q, k, v, out, c->lse, c->n_heads, c->seq_len, c->d_head, scale,
-                            causal, stream);
+  const int st = dfattn_fwd_train(q, k, v, out, c->lse, c->workspace, c->workspace_bytes, c->n_heads,
+                                  c->seq_len, c->d_head, scale, causal, stream);
   if (st == DFATTN_OK) {
     c->last_q = q;
     c->last_k = k;
@@ -99,8 +102,11 @@ int run_backward(dfattn_context *c, const float *q, const float *k, const float 
     if (st != DFATTN_OK) return st;
     o = c->own_out;
   }
-  return dfattn_bwd(q, k, v, o, d_out, c->lse, d_q, d_k, d_v, c->workspace, c->workspace_bytes,
-                    c->n_heads, c->seq_len, c->d_head, scale, causal, stream);
+  const int st = dfattn_bwd_preprocess(q, k, v, o, d_out, c->lse, c->workspace, c->workspace_bytes,
+                                       c->n_heads, c->seq_len, c->d_head, scale, DFATTN_BWD_QKV_SAVED, stream);
+  if (st != DFATTN_OK) return st;
+  return dfattn_bwd_main(q, k, v, o, d_out, c->lse, d_q, d_k, d_v, c->workspace, c->workspace_bytes,
+                         c->n_heads, c->seq_len, c->d_head, scale, causal, stream);
 }
 
 void free_all(dfattn_context *c) {

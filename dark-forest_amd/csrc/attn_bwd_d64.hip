@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
     const float *__restrict__ blockmax, float *__restrict__ sigma_out, float *__restrict__ lse2n,
     float *__restrict__ deltan,
     half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
-    int H, int S, int n_pre_blocks, float c2) {
+    int H, int S, int n_pre_blocks, float c2, int convert_qkv) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int head = blockIdx.y;
   const int row = blockIdx.x * 64 + (tid >> 2);
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok);
+    for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok && (t == 3 || convert_qkv));
   float gmax = 0.f;
   for (int i = lane; i < n_pre_blocks; i += 64) gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
   const float sigma = pow2_scale(wave_max(gmax));
@@ -191,7 +191,8 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
   }
   half_t *out[4] = {q16, k16, v16, do16};
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 4; ++t) {
+    if (t < 3 && !convert_qkv) continue;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       half4_t lo, hi;
@@ -208,6 +209,7 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
       *reinterpret_cast<half8_t *>(out[t] + dst + 8 * i) =
           half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+  }
 }
 
 // Relative cost of one step of each item kind (measured at C2: a dK/dV step,
@@ -761,9 +763,17 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
 
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) { return ws_layout(n_heads, seq_len).total; }
 
+void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16) {
+  const WsLayout w = ws_layout(n_heads, seq_len);
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  *q16 = reinterpret_cast<half_t *>(ws + w.q16);
+  *k16 = reinterpret_cast<half_t *>(ws + w.k16);
+  *v16 = reinterpret_cast<half_t *>(ws + w.v16);
+}
+
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
                               const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
-                              float scale, hipStream_t stream) {
+                              float scale, hipStream_t stream, bool qkv_saved) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   float *delta = reinterpret_cast<float *>(ws);
@@ -777,7 +787,7 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
                      reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
                      reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, pre_blocks(seq_len),
-                     scale * kLog2e);
+                     scale * kLog2e, qkv_saved ? 0 : 1);
   return hipGetLastError();
 }
 

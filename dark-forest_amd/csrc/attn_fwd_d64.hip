@@ -66,10 +66,18 @@ __device__ __forceinline__ half4_t lds_tr4(const unsigned char *p) {
                                          (lds_i16x4 *)(const __attribute__((address_space(3))) unsigned char *)p));
 }
 
+// Q16, K16, V16 (all null, or none): the training forward also writes c2*Q,
+// K and V as fp16 into these [H][S][64] copies, rounded exactly as the
+// backward would round them, so the backward need not convert them again.
+// Each workgroup writes its own 128 rows of c2*Q from its prologue
+// registers. The K and V rows are copied at the end by the workgroups with
+// little causal work: the one with query tile i < n-1-i copies the rows of
+// tiles i and n-1-i, so the longest workgroups, which set the makespan, do
+// no extra loads (without causal masking every workgroup copies its own).
 __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     float *__restrict__ O, float *__restrict__ LSE, int H, int S, float qscale, int causal,
-    int n_qtiles) {
+    int n_qtiles, half_t *__restrict__ Q16, half_t *__restrict__ K16, half_t *__restrict__ V16) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -104,6 +112,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   // then reads its Q^T fragments from there.
   half8_t qf[4];
   float4 qraw[kQF4];
+  const bool save = Q16 != nullptr;
   {
     const unsigned rows = (unsigned)max(0, min(S - q_blk0, kBM));
     const size_t base = (size_t)min(q_blk0, S) * ld;
@@ -291,7 +300,10 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
 #pragma unroll
     for (int k = 0; k < kQF4; ++k) {
       const int idx = tid + k * kThreads;
-      *reinterpret_cast<half4_t *>(qt + tile_off(idx >> 4, (idx & 15) * 4)) = round_scaled4(qraw[k], qscale);
+      const half4_t qh = round_scaled4(qraw[k], qscale);
+      *reinterpret_cast<half4_t *>(qt + tile_off(idx >> 4, (idx & 15) * 4)) = qh;
+      const int row = q_blk0 + (idx >> 4);
+      if (save && row < S) *reinterpret_cast<half4_t *>(Q16 + ((size_t)head * S + row) * kD + (idx & 15) * 4) = qh;
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p) store_rows(kstage(p), kp[p]);
@@ -419,6 +431,42 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   }
   __syncthreads();  // the merge below reuses the rings
 
+  if (save) {
+    // K and V rows of query tile qt as fp16 (rows past S are not written).
+    auto copy_kv = [&](int qt) {
+      const int r0 = qt * kBM;
+      const unsigned rows = (unsigned)max(0, min(S - r0, kBM));
+      const size_t base = (size_t)min(r0, S) * ld;
+      const auto rk = buffer_rsrc(K + base, rows * (unsigned)ld * 4);
+      const auto rv = buffer_rsrc(V + base, rows * (unsigned)ld * 4);
+      float4 kx[kQF4], vx[kQF4];
+#pragma unroll
+      for (int k = 0; k < kQF4; ++k) {
+        const int idx = tid + k * kThreads;
+        const int off = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
+        kx[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        vx[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+      }
+#pragma unroll
+      for (int k = 0; k < kQF4; ++k) {
+        const int idx = tid + k * kThreads;
+        const int row = r0 + (idx >> 4);
+        if (row < S) {
+          const size_t dst = ((size_t)head * S + row) * kD + (idx & 15) * 4;
+          *reinterpret_cast<half4_t *>(K16 + dst) = to_half4(kx[k]);
+          *reinterpret_cast<half4_t *>(V16 + dst) = to_half4(vx[k]);
+        }
+      }
+    };
+    const int mirror = n_qtiles - 1 - qtile;
+    if (!causal || qtile == mirror) {
+      copy_kv(qtile);
+    } else if (qtile < mirror) {
+      copy_kv(qtile);
+      copy_kv(mirror);
+    }
+  }
+
 
   // Merge the key halves: wave qg+4 hands (o, m, l) to wave qg through LDS.
   float *mbuf = reinterpret_cast<float *>(lds_raw) + (size_t)qg * kMergeRegs * 64;
@@ -467,11 +515,13 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
 
 hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float *o, float *lse,
                           int n_heads, int seq_len, float scale, bool causal,
-                          hipStream_t stream) {
+                          hipStream_t stream, void *bwd_workspace) {
   const int n_qtiles = (seq_len + kBM - 1) / kBM;
   const dim3 grid((unsigned)(n_qtiles * n_heads));
+  half_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
+  if (bwd_workspace != nullptr) bwd_ws_qkv_copies(bwd_workspace, n_heads, seq_len, &q16, &k16, &v16);
   hipLaunchKernelGGL(fwd_d64_kernel, grid, dim3(kThreads), 0, stream, q, k, v, o, lse, n_heads,
-                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles);
+                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles, q16, k16, v16);
   return hipGetLastError();
 }
 

@@ -241,12 +241,29 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o, c
   return record_hip(err, "attention backward launch");
 }
 
+int dfattn_fwd_train(const float *q, const float *k, const float *v, float *o, float *lse,
+                     void *workspace, size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
+                     uint32_t d_head, float scale, uint32_t causal, void *stream) {
+  const char *fn = "dfattn_fwd_train";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, lse});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st != DFATTN_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Without the fast path there are no copies to write: a backward that
+  // takes its fast path has every pointer aligned, so this forward took it too.
+  if (!fast_path(d_head, {q, k, v, o, lse})) return fwd_impl(q, k, v, o, lse, n_heads, seq_len, d_head, scale, causal, s);
+  return record_hip(dfattn::launch_fwd_d64(q, k, v, o, lse, (int)n_heads, (int)seq_len, scale, causal != 0, s,
+                                           workspace),
+                    "attention forward launch");
+}
+
 // The split backward decides the fast path from q, k, v, o and d_o in both
 // phases, so main takes it only when preprocess filled the workspace.
 int dfattn_bwd_preprocess(const float *q, const float *k, const float *v, const float *o,
                           const float *d_o, const float *lse, void *workspace, size_t workspace_bytes,
                           uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale,
-                          void *stream) {
+                          uint32_t flags, void *stream) {
   const char *fn = "dfattn_bwd_preprocess";
   int st = check_shape(fn, n_heads, seq_len, d_head);
   if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse});
@@ -254,8 +271,11 @@ int dfattn_bwd_preprocess(const float *q, const float *k, const float *v, const 
   if (st != DFATTN_OK) return st;
   // The generic kernel recomputes its row statistics itself: nothing to do.
   if (!fast_path(d_head, {q, k, v, o, d_o})) return DFATTN_OK;
+  if ((flags & ~(uint32_t)DFATTN_BWD_QKV_SAVED) != 0)
+    return record_error(DFATTN_ERR_FLAGS, std::string(fn) + ": unknown flag bits");
   return record_hip(dfattn::launch_bwd_pre_d64(q, k, v, o, d_o, lse, workspace, (int)n_heads, (int)seq_len,
-                                               scale, static_cast<hipStream_t>(stream)),
+                                               scale, static_cast<hipStream_t>(stream),
+                                               (flags & DFATTN_BWD_QKV_SAVED) != 0),
                     "attention backward preprocess launch");
 }
 
@@ -289,6 +309,7 @@ const char *dfattn_status_string(int status) {
     case DFATTN_ERR_OVERFLOW: return "shape overflow";
     case DFATTN_ERR_WORKSPACE: return "workspace too small";
     case DFATTN_ERR_HIP: return "HIP error";
+    case DFATTN_ERR_FLAGS: return "unknown flags";
     default: return "unknown status";
   }
 }

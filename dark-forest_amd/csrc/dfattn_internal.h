@@ -238,13 +238,18 @@ __device__ __forceinline__ half8_t acc_to_slots(const f32x16 &blk, int half_sel)
 
 // ---- internal launch API (host side, all asynchronous on `stream`) -------
 
-// Forward, D = 64, MFMA. q/k/v/o 16-byte aligned. lse may be null.
+// Forward, D = 64, MFMA. q/k/v/o 16-byte aligned. lse may be null. With a
+// backward workspace (bwd_workspace_bytes_d64 bytes), the forward also
+// writes the backward's fp16 copies of c2*Q, K and V into it (see
+// launch_bwd_pre_d64's qkv_saved).
 hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float *o,
                           float *lse, int n_heads, int seq_len, float scale, bool causal,
-                          hipStream_t stream);
+                          hipStream_t stream, void *bwd_workspace = nullptr);
 
 // Backward, D = 64, MFMA. Needs bwd_workspace_bytes_d64() of workspace.
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len);
+// Where the fp16 copies of c2*Q, K and V sit in a backward workspace.
+void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16);
 hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const float *o,
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,
@@ -252,9 +257,12 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
 // The two phases of launch_bwd_d64: the workspace (Delta, the dO range and
 // the fp16 operand copies), then the main kernel, which reads only the
 // workspace, lse and its outputs.
+// qkv_saved: the workspace already holds the copies of c2*Q, K and V that a
+// launch_fwd_d64 with this workspace wrote for the same q, k, v and scale;
+// only dO is converted.
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
                               const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
-                              float scale, hipStream_t stream);
+                              float scale, hipStream_t stream, bool qkv_saved = false);
 hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
                                int n_heads, int seq_len, float scale, bool causal, hipStream_t stream);
 

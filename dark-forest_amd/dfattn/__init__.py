@@ -49,7 +49,8 @@ SYMBOLS = {
     "dfattn_fwd": (ctypes.c_int, [_P] * 5 + [_U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
     "dfattn_bwd": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
-    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _P]),
+    "dfattn_fwd_train": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dfattn_last_error": (ctypes.c_int, []),
@@ -156,6 +157,23 @@ def attention_forward(q, k, v, n_heads, scale=None, causal=True, out=None, lse=N
     return out, lse
 
 
+def forward_train(q, k, v, n_heads, workspace, scale=None, causal=True, out=None, lse=None, stream=None):
+    """attention_forward that also leaves the backward's fp16 copies of Q, K, V in `workspace`
+    (dfattn_fwd_train); follow with backward_preprocess(..., flags=BWD_QKV_SAVED)."""
+    torch = _torch()
+    seq_len, d_head = _dims(q, n_heads)
+    if scale is None:
+        scale = d_head ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty((n_heads, seq_len), dtype=torch.float32, device=q.device)
+    _check(lib().dfattn_fwd_train(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out), _dev_ptr(lse),
+                                  _dev_ptr(workspace), workspace.numel() * workspace.element_size(), n_heads,
+                                  seq_len, d_head, scale, int(bool(causal)), _stream_ptr(stream)))
+    return out, lse
+
+
 def bwd_workspace_bytes(n_heads, seq_len, d_head) -> int:
     return int(lib().dfattn_bwd_workspace_bytes(n_heads, seq_len, d_head))
 
@@ -180,15 +198,18 @@ def attention_backward(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d
     return d_q, d_k, d_v
 
 
-def backward_preprocess(q, k, v, o, d_o, lse, workspace, n_heads, scale=None, stream=None):
+BWD_QKV_SAVED = 1  # DFATTN_BWD_QKV_SAVED
+
+
+def backward_preprocess(q, k, v, o, d_o, lse, workspace, n_heads, scale=None, flags=0, stream=None):
     """First phase of attention_backward (row statistics, the dO range and the fp16 operand
-    copies, all in the workspace)."""
+    copies, all in the workspace); flags=BWD_QKV_SAVED after forward_train."""
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5
     _check(lib().dfattn_bwd_preprocess(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o),
                                        _dev_ptr(lse), _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
-                                       n_heads, seq_len, d_head, scale, _stream_ptr(stream)))
+                                       n_heads, seq_len, d_head, scale, int(flags), _stream_ptr(stream)))
 
 
 def backward_main(q, k, v, o, d_o, lse, d_q, d_k, d_v, workspace, n_heads, scale=None, causal=True, stream=None):

@@ -50,8 +50,12 @@ typedef enum dfattn_status {
   DFATTN_ERR_HEAD_DIM = -4,       /* d_head outside 1..=128                     */
   DFATTN_ERR_OVERFLOW = -5,       /* seq_len*n_heads*d_head does not fit        */
   DFATTN_ERR_WORKSPACE = -6,      /* workspace NULL or smaller than required    */
-  DFATTN_ERR_HIP = -7             /* a HIP launch failed (see dfattn_last_error) */
+  DFATTN_ERR_HIP = -7,            /* a HIP launch failed (see dfattn_last_error) */
+  DFATTN_ERR_FLAGS = -8           /* unknown bits in a flags argument           */
 } dfattn_status;
+
+/* Flags of dfattn_bwd_preprocess. */
+#define DFATTN_BWD_QKV_SAVED 1u /* the workspace holds dfattn_fwd_train's copies */
 
 /* ---- Group 1: the reference's launcher symbols ---------------------------
  * Same signatures as the reference. Launches go to the legacy default (null)
@@ -108,6 +112,19 @@ int dfattn_fwd(const float *q, const float *k, const float *v, float *o,
                float *lse, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                float scale, uint32_t causal, void *stream);
 
+/* Forward of a training step: everything dfattn_fwd does (lse required),
+ * and, on the d_head = 64 fast path, the backward's fp16 copies of
+ * scale*log2(e)*Q, K and V written into `workspace` (which must hold
+ * dfattn_bwd_workspace_bytes()), rounded exactly as the backward rounds
+ * them. A later dfattn_bwd_preprocess with DFATTN_BWD_QKV_SAVED on the same
+ * q, k, v, scale and workspace then converts only dO (about 56 MB less
+ * traffic at H = 12, S = 4096). No reference counterpart: the reference's
+ * backward recomputes the forward from scratch (attention_fused.cu:390-516). */
+int dfattn_fwd_train(const float *q, const float *k, const float *v, float *o,
+                     float *lse, void *workspace, size_t workspace_bytes,
+                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                     float scale, uint32_t causal, void *stream);
+
 /* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len * d_head)
  * (row statistics Delta_i = dO_i . O_i, a per-head dO range scale, the row
  * statistics as the main phase's products take them, and fp16 copies of the
@@ -132,13 +149,18 @@ int dfattn_bwd(const float *q, const float *k, const float *v, const float *o,
  * with one workspace). Preprocess reads Q, K, V, O, dO and lse and fills
  * the workspace (row statistics and the fp16 operand copies); main reads
  * the workspace and writes dQ, dK, dV. Pass both phases the same
- * q, k, v, o, d_o, lse, workspace and scale. No reference counterpart: the
+ * q, k, v, o, d_o, lse, workspace and scale. flags: 0, or
+ * DFATTN_BWD_QKV_SAVED when a dfattn_fwd_train with the same q, k, v,
+ * scale and workspace has run and neither q, k, v nor the workspace has
+ * changed since (preprocess then converts only dO). No reference
+ * counterpart: the
  * reference backward is one kernel without saved statistics
  * (attention_fused.cu:390-516).                                             */
 int dfattn_bwd_preprocess(const float *q, const float *k, const float *v,
                           const float *o, const float *d_o, const float *lse,
                           void *workspace, size_t workspace_bytes, uint32_t n_heads,
-                          uint32_t seq_len, uint32_t d_head, float scale, void *stream);
+                          uint32_t seq_len, uint32_t d_head, float scale, uint32_t flags,
+                          void *stream);
 int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     const float *o, const float *d_o, const float *lse, float *d_q,
                     float *d_k, float *d_v, void *workspace, size_t workspace_bytes,

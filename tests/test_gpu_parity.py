@@ -344,3 +344,25 @@ def test_split_backward_phases_match_dfattn_bwd(device):
     torch.cuda.synchronize()
     for name, a, b in zip(("dq", "dk", "dv"), got, ref):
         assert_close(f"split, unaligned o, {name}", host(a), host(b), scaled=True)
+
+
+def test_training_forward_copies_match_the_full_conversion(device):
+    """dfattn_fwd_train + preprocess(QKV_SAVED) + main give dfattn_fwd + dfattn_bwd's outputs bit for bit,
+    causal and full, including a ragged length (rows past S are never written)."""
+    import torch
+
+    for seq_len, causal in ((384, True), (200, False), (1000, True)):
+        say(f"training forward S={seq_len} causal={causal}")
+        x = O.seeded_inputs(seq_len, 12, 64, 3400 + seq_len)
+        q, k, v, g = (to_dev(x[n], device) for n in ("q", "k", "v", "do"))
+        o_ref, lse_ref = dfattn.attention_forward(q, k, v, 12, 0.125, causal)
+        ref = dfattn.attention_backward(q, k, v, o_ref, g, lse_ref, 12, 0.125, causal)
+        ws = torch.full((dfattn.bwd_workspace_bytes(12, seq_len, 64) // 4,), float("nan"), device=device)
+        o, lse = dfattn.forward_train(q, k, v, 12, ws, 0.125, causal)
+        got = [torch.empty_like(q) for _ in range(3)]
+        dfattn.backward_preprocess(q, k, v, o, g, lse, ws, 12, 0.125, flags=dfattn.BWD_QKV_SAVED)
+        dfattn.backward_main(q, k, v, o, g, lse, *got, ws, 12, 0.125, causal)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
