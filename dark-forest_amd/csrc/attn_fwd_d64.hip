@@ -70,10 +70,10 @@ __device__ __forceinline__ half4_t lds_tr4(const unsigned char *p) {
 // K and V as fp16 into these [H][S][64] copies, rounded exactly as the
 // backward would round them, so the backward need not convert them again.
 // Each workgroup writes its own 128 rows of c2*Q from its prologue
-// registers. The K and V rows are copied at the end by the workgroups with
-// little causal work: the one with query tile i < n-1-i copies the rows of
-// tiles i and n-1-i, so the longest workgroups, which set the makespan, do
-// no extra loads (without causal masking every workgroup copies its own).
+// registers. Under causal masking the K and V rows of its own query tile are
+// the last key tiles the workgroup stages, and it writes them from LDS after
+// the loop; without masking each workgroup copies those rows from the
+// inputs at the end.
 __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     float *__restrict__ O, float *__restrict__ LSE, int H, int S, float qscale, int causal,
@@ -432,9 +432,28 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   __syncthreads();  // the merge below reuses the rings
 
   if (save) {
-    // K and V rows of query tile qt as fp16 (rows past S are not written).
-    auto copy_kv = [&](int qt) {
-      const int r0 = qt * kBM;
+    if (causal) {
+      // The key tiles of the workgroup's own rows (2*qtile and, below S,
+      // 2*qtile+1) were the loop's last and still sit in their ring stages,
+      // rounded to fp16 exactly as the backward rounds K and V: one 16-byte
+      // granule per thread and tile goes out (rows past S are not written).
+      const int r = tid >> 3, g = tid & 7;
+      for (int kt = 2 * qtile; kt < n_tiles; ++kt) {
+        const int row = kt * kBN + r;
+        const int off = 2 * tile_off(r, 8 * g);
+        const half8_t kx = *reinterpret_cast<const half8_t *>(kstage(kt) + off);
+        const half8_t vx = *reinterpret_cast<const half8_t *>(vstage(kt) + off);
+        if (row < S) {
+          const size_t dst = ((size_t)head * S + row) * kD + 8 * g;
+          *reinterpret_cast<half8_t *>(K16 + dst) = kx;
+          *reinterpret_cast<half8_t *>(V16 + dst) = vx;
+        }
+      }
+      __syncthreads();  // the merge below overwrites the K ring
+    } else {
+      // Every workgroup sees every key tile: each copies the K and V rows of
+      // its own query tile from the inputs.
+      const int r0 = q_blk0;
       const unsigned rows = (unsigned)max(0, min(S - r0, kBM));
       const size_t base = (size_t)min(r0, S) * ld;
       const auto rk = buffer_rsrc(K + base, rows * (unsigned)ld * 4);
@@ -457,16 +476,8 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
           *reinterpret_cast<half4_t *>(V16 + dst) = to_half4(vx[k]);
         }
       }
-    };
-    const int mirror = n_qtiles - 1 - qtile;
-    if (!causal || qtile == mirror) {
-      copy_kv(qtile);
-    } else if (qtile < mirror) {
-      copy_kv(qtile);
-      copy_kv(mirror);
     }
   }
-
 
   // Merge the key halves: wave qg+4 hands (o, m, l) to wave qg through LDS.
   float *mbuf = reinterpret_cast<float *>(lds_raw) + (size_t)qg * kMergeRegs * 64;
