@@ -67,6 +67,8 @@ int check_dims(uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   size_t dm = 0, e = 0, b = 0;
   if (__builtin_mul_overflow((size_t)n_heads, (size_t)d_head, &dm))
     return fail(DFATTN_ERR_OVERFLOW, "d_model overflow");
+  if (n_heads > 65535 || seq_len > (1u << 30))  // the attention entry points' limits
+    return fail(DFATTN_ERR_OVERFLOW, "attention shape is too large");
   if (__builtin_mul_overflow((size_t)seq_len, dm, &e) || __builtin_mul_overflow(e, sizeof(float), &b))
     return fail(DFATTN_ERR_OVERFLOW, "attention shape is too large");
   return DFATTN_OK;

@@ -49,6 +49,7 @@ static_assert(kThreads * 8 == kTile, "one half8 per thread clears a tile");
 // Merge buffer: per partner wave, 32 output registers + max + sum, lane-major.
 constexpr int kMergeRegs = 34;
 constexpr float kRescale = 8.f;  // log2 headroom of the softmax reference point
+constexpr float kRescaleSum = 256.f;  // 2^kRescale
 constexpr int kRingBytes = 2 * kStages * kTileBytes;
 constexpr int kMergeBytes = 4 * kMergeRegs * 64 * 4;
 // After the rings: the workgroup's 128 Q rows as a [128][64] fp16 tile (c2 Q),
@@ -156,9 +157,8 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   float4 kreg[2][kF4], vreg[2][kF4];
   auto load_rows = [&](const float *X, int t, float4 (&xr)[kF4]) {
     const int kv0 = t * kBN;
-    const long long rem = (long long)(S - kv0) * ld * 4;
-    const unsigned nrec = rem <= 0 ? 0u : (unsigned)min(rem, (long long)kBN * ld * 4);
-    const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ld, nrec);
+    const int rows = uniform_clamp0<kBN>(S - kv0);  // (n_heads <= 65535: 64 rows span < 2^30 bytes)
+    const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ld, (unsigned)rows * (unsigned)(ld * 4));
 #pragma unroll
     for (int i = 0; i < kF4; ++i)
       xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff[i], 0, 0));
@@ -402,11 +402,17 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     read_v(p + kStages - 1, vf);
     f32x16 sn = scores(kf);
     pv(vf, pprev);
-    const float mx = row_max(s);
     probs(s, pf);
     const float psum = rowsum(pf);
     stage_tiles(t, p, std::integral_constant<int, (p + 1) & 1>{}, true);
-    softmax_fix(s, sn, pf, mx, psum, std::true_type{});
+    // Every P is >= 0, so a lane's sum bounds its largest P, and a score more
+    // than kRescale above the reference point makes P >= 2^kRescale: the
+    // exact row maximum (and the rescale test) is needed only when a sum
+    // reaches that, or before the first reference point.
+    if (__any(psum >= kRescaleSum || m == -INFINITY))
+      softmax_fix(s, sn, pf, row_max(s), psum, std::true_type{});
+    else
+      l += psum;
     s = sn;
     pprev[0] = pf[0];
     pprev[1] = pf[1];

@@ -52,6 +52,12 @@ bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 // Shape checks shared by every entry point (the reference's are in
 // AttentionContext::new_shared, darkforest-cuda/src/lib.rs:1981-1989).
+// Launch grids keep one head per row of a 2-D grid, whose second dimension
+// holds at most 65535 blocks (the reference's grids, attention_fused.cu:239,
+// have the same bound); this also keeps every offset of a 128-row tile of the
+// [S, H*64] inputs inside 31 bits.
+constexpr uint32_t kMaxHeads = 65535;
+
 int check_shape(const char *fn, uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   if (n_heads == 0 || seq_len == 0)
     return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": n_heads and seq_len must be >= 1");
@@ -61,7 +67,7 @@ int check_shape(const char *fn, uint32_t n_heads, uint32_t seq_len, uint32_t d_h
   if (__builtin_mul_overflow((size_t)n_heads, (size_t)d_head, &dm) ||
       __builtin_mul_overflow((size_t)seq_len, dm, &elems) ||
       __builtin_mul_overflow(elems, sizeof(float), &bytes) || seq_len > (1u << 30) ||
-      n_heads > (1u << 20))
+      n_heads > kMaxHeads)
     return record_error(DFATTN_ERR_OVERFLOW, std::string(fn) + ": attention shape is too large");
   return DFATTN_OK;
 }
@@ -204,7 +210,7 @@ int dfattn_fwd(const float *q, const float *k, const float *v, float *o, float *
 
 size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   if (n_heads == 0 || seq_len == 0 || d_head == 0 || d_head > 128 || seq_len > (1u << 30) ||
-      n_heads > (1u << 20))
+      n_heads > kMaxHeads)
     return 0;
   return dfattn::bwd_workspace_bytes_d64((int)n_heads, (int)seq_len);
 }

@@ -79,6 +79,14 @@ __device__ __forceinline__ auto buffer_rsrc(const void *p, unsigned nrec) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, __builtin_amdgcn_readfirstlane(nrec),
                                            kBufferFlags);
 }
+// min(max(x, 0), HI) of a wave-uniform x, on the scalar unit: the compiler
+// lowers the clamp to a vector med3 followed by readfirstlane otherwise.
+template <int HI>
+__device__ __forceinline__ int uniform_clamp0(int x) {
+  int r;
+  asm("s_max_i32 %0, %1, 0\n\ts_min_i32 %0, %0, %2" : "=&s"(r) : "s"(x), "n"(HI) : "scc");
+  return r;
+}
 constexpr float kLn2 = 0.6931471805599453f;
 
 // D = 64 fast path: one 32x32x16 fp16 MFMA (fp32 accumulate). Operand

@@ -48,7 +48,8 @@ typedef enum dfattn_status {
   DFATTN_ERR_MISALIGNED = -2,     /* a tensor pointer is not 4-byte aligned     */
   DFATTN_ERR_SHAPE = -3,          /* n_heads == 0 or seq_len == 0               */
   DFATTN_ERR_HEAD_DIM = -4,       /* d_head outside 1..=128                     */
-  DFATTN_ERR_OVERFLOW = -5,       /* seq_len*n_heads*d_head does not fit        */
+  DFATTN_ERR_OVERFLOW = -5,       /* seq_len*n_heads*d_head does not fit, or    */
+                                  /* seq_len > 2^30 or n_heads > 65535          */
   DFATTN_ERR_WORKSPACE = -6,      /* workspace NULL or smaller than required    */
   DFATTN_ERR_HIP = -7,            /* a HIP launch failed (see dfattn_last_error) */
   DFATTN_ERR_FLAGS = -8           /* unknown bits in a flags argument           */

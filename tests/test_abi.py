@@ -54,7 +54,7 @@ def fwd(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=None, h=12, s=128, d=64):
 @pytest.mark.parametrize("kwargs,status", [
     (dict(q=None), -1), (dict(o=None), -1), (dict(v=ODD), -2), (dict(lse=ODD), -2),
     (dict(h=0), -3), (dict(s=0), -3), (dict(d=0), -4), (dict(d=129), -4),
-    (dict(h=1 << 21), -5), (dict(s=(1 << 30) + 1), -5),
+    (dict(h=1 << 21), -5), (dict(h=65536), -5), (dict(s=(1 << 30) + 1), -5),
 ])
 def test_forward_validation(kwargs, status):
     lib = dfattn.lib()
@@ -134,7 +134,7 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 # ---------------------------------------------------------------- the context mirror (lib.rs:1949-2368)
 @pytest.mark.parametrize("dims,status", [
     ((12, 128, 0), -4), ((12, 128, 129), -4), ((0, 128, 64), -3), ((12, 0, 64), -3),
-    ((2 ** 32 - 1, 2 ** 32 - 1, 128), -5),
+    ((2 ** 32 - 1, 2 ** 32 - 1, 128), -5), ((65536, 16, 64), -5),
 ])
 def test_context_create_validates_like_new_shared(dims, status):
     """AttentionContext::new_shared's checks (lib.rs:1981-1989) run before any device allocation."""
