@@ -339,7 +339,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int dma_off = drow * 128 + (((lane & 7) ^ tile_swz(drow)) << 4);
   auto dma_block = [&](int i, int st) {
     const int qb0 = (first_qb + i) * kQBlock;
-    const int rows = max(0, min(S - qb0, kQBlock));
+    const int rows = uniform_clamp0<kQBlock>(S - qb0);
     const size_t base = (size_t)head * S + min(qb0, S);
     const unsigned qt = lds_addr32(stage_base(st) + wave * 1024);
     lds_fetch16(sgpr_rsrc(a.Q16 + base * kD, (unsigned)rows * kD * 2), qt, dma_off);
@@ -554,7 +554,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   auto dma_tile = [&](int t, int st) {
     const unsigned kt = lds_addr32(lds_raw + st * kStageBytes + wave * 1024);
     const int row0 = t * kKTile;
-    const unsigned nrec = (unsigned)max(0, min(S - row0, kKTile)) * kD * 2;
+    const unsigned nrec = (unsigned)uniform_clamp0<kKTile>(S - row0) * kD * 2;
     const size_t base = ((size_t)head * S + min(row0, S)) * kD;
     lds_fetch16(sgpr_rsrc(a.K16 + base, nrec), kt, dma_off);
     lds_fetch16(sgpr_rsrc(a.V16 + base, nrec), kt + kTile * 2, dma_off);
@@ -563,11 +563,10 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   f32x16 dq[2];
   dq[0] = dq[1] = f32x16{};
 
-  // One tile. `masked`: the tile may hold the causal diagonal or the end of
-  // the keys; a wave that sees none of it skips it.
-  auto compute = [&](int t, int st, bool masked) {
-    const int k0 = t * kKTile + kh * 32;  // first key of this wave's half tile
-    if (masked && !(wave_active && k0 < S && (!a.causal || k0 <= wave_qlast))) return;
+  // Scores of the tile in stage st: S^T - lse2 and dP^T - Delta, register r
+  // is key k0 + 8*(r/4) + 4*hh + r%4 (lane = query); the chains start from
+  // the lane's -lse2 / -Delta.
+  auto scores = [&](int st, f32x16 &s, f32x16 &dp) {
     const half_t *kt = stage_base(st);
     const half_t *vt = kt + kTile;
     half8_t ka[4], va[4];
@@ -576,15 +575,19 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
       ka[ds] = *reinterpret_cast<const half8_t *>(kt + koff[ds]);
       va[ds] = *reinterpret_cast<const half8_t *>(vt + koff[ds]);
     }
-    // S^T - lse2 and dP^T - Delta: register r is key k0 + 8*(r/4) + 4*hh +
-    // r%4 (lane = query); the chains start from the lane's -lse2 / -Delta.
-    f32x16 s = mfma32x32x16(ka[0], qf[0], negL);
-    f32x16 dp = mfma32x32x16(va[0], gf[0], negD);
+    s = mfma32x32x16(ka[0], qf[0], negL);
+    dp = mfma32x32x16(va[0], gf[0], negD);
 #pragma unroll
     for (int ds = 1; ds < 4; ++ds) {
       s = mfma32x32x16(ka[ds], qf[ds], s);
       dp = mfma32x32x16(va[ds], gf[ds], dp);
     }
+  };
+  // The gradient work of tile t (stage st) from its scores: dS = P * (dP -
+  // Delta) (the mask first when `masked`), then dQ^T += K^T dS^T over this
+  // wave's two key steps.
+  auto grads = [&](int t, int st, f32x16 &s, f32x16 &dp, bool masked) {
+    const half_t *kt = stage_base(st);
     half8_t ktr[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -593,20 +596,31 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
         const half4_t lo = tile_tr4_at(kt, ktoff[j][db][0]), hi = tile_tr4_at(kt, ktoff[j][db][1]);
         ktr[j][db] = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
-    if (masked && k0 + 31 > key_lim_lo) {
+    if (masked) {
+      const int k0 = t * kKTile + kh * 32;
+      if (k0 + 31 > key_lim_lo) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
+        for (int r = 0; r < 16; ++r)
+          if (k0 + (r >> 2) * 8 + hh * 4 + (r & 3) > key_lim) s[r] = -INFINITY;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) dp[r] *= fast_exp2(s[r]);
-    // dQ^T += K^T dS^T over this wave's two key steps.
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const half8_t dsf = acc_to_slots(dp, j);
 #pragma unroll
       for (int db = 0; db < 2; ++db) dq[db] = mfma32x32x16(ktr[j][db], dsf, dq[db]);
     }
+  };
+  // One tile, unpipelined. `masked`: the tile may hold the causal diagonal or
+  // the end of the keys; a wave that sees none of it skips it.
+  auto compute = [&](int t, int st, bool masked) {
+    const int k0 = t * kKTile + kh * 32;  // first key of this wave's half tile
+    if (masked && !(wave_active && k0 < S && (!a.causal || k0 <= wave_qlast))) return;
+    f32x16 s, dp;
+    scores(st, s, dp);
+    grads(t, st, s, dp, masked);
   };
 
   // Prologue: the workgroup's c2*Q and sigma*dO rows, its rows' -lse*log2(e)
@@ -626,7 +640,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   }
 #pragma unroll
   for (int p = 0; p < 3; ++p) dma_tile(p, p);
-  lds_fetch_barrier<4>();
+  lds_fetch_barrier<2>();  // tiles 0 and 1 have landed
   {
     // The lane's -lse*log2(e) and -Delta*sigma (rows past S: P = 0), and the
     // (c2 Q)^T and (sigma dO)^T fragments (B operands): lane c holds query
@@ -647,22 +661,41 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
     }
   }
 
-  auto iter = [&](int t, auto u) {
-    constexpr int q = decltype(u)::value;
-    // Tile t+3 goes into its stage (last read in iteration t-1) and tile t+5
-    // is fetched before the products of tile t, so the fetch has most of
-    // three iterations to arrive.
-    dma_tile(t + 3, (q + 3) & 3);
-    compute(t, q, false);
-    lds_fetch_barrier<4>();  // tile t+1 has landed; tiles t+2, t+3 may be in flight
-  };
+  // Unmasked tiles 0 .. n_full-1, software-pipelined: iteration t issues the
+  // scores of tile t+1 (stage t+1) before the gradient work of tile t
+  // (stage t), which does not depend on them, so the products of one run
+  // beside the exponentials of the other. Tile t+3 is fetched at the start
+  // of iteration t into the stage last read in iteration t-1; the barrier at
+  // the end leaves tile t+2 landed, with tile t+3 in flight.
   int t = 0;
-  for (; t + 4 <= n_full; t += 4) {
-    iter(t, Const<0>{});
-    iter(t + 1, Const<1>{});
-    iter(t + 2, Const<2>{});
-    iter(t + 3, Const<3>{});
+  if (n_full > 0) {
+    f32x16 s, dp;
+    scores(0, s, dp);
+    auto iter = [&](int tt, int st, int stn) {
+      dma_tile(tt + 3, (st + 3) & 3);
+      f32x16 sn, dpn;
+      scores(stn, sn, dpn);
+      grads(tt, st, s, dp, false);
+      s = sn;
+      dp = dpn;
+      lds_fetch_barrier<2>();
+    };
+    for (; t + 4 < n_full; t += 4) {
+      iter(t, 0, 1);
+      iter(t + 1, 1, 2);
+      iter(t + 2, 2, 3);
+      iter(t + 3, 3, 0);
+    }
+    for (; t + 1 < n_full; ++t) iter(t, t & 3, (t + 1) & 3);
+    // The last unmasked tile: its gradient work, and the fetch that
+    // iteration t would have issued.
+    if (t + 3 < n_tiles) dma_tile(t + 3, (t + 3) & 3);
+    grads(t, t & 3, s, dp, false);
+    lds_fetch_barrier<0>();
+    ++t;
   }
+  // The rest (masked tiles, and the keys' end), unpipelined: tile t has
+  // landed at the top of each iteration.
   for (; t < n_tiles; ++t) {
     if (t + 3 < n_tiles) dma_tile(t + 3, (t + 3) & 3);
     compute(t, t & 3, true);
