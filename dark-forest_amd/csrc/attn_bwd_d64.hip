@@ -348,14 +348,6 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
       lds_fetch4(sgpr_rsrc((wave_u == 0 ? a.lse2n : a.deltan) + base, (unsigned)rows * 4),
                  lds_addr32(stage_base(st) + 2 * kTile * 2 + wave_u * kQBlock * 4), lane * 4);
   };
-  // Barrier after block i+1 has landed, with the fetches of blocks i+2 and
-  // i+3 (two per block, three for waves 0 and 1) still in flight.
-  auto fetch_barrier = [&]() {
-    if (wave_u < 2)
-      lds_fetch_barrier<6>();
-    else
-      lds_fetch_barrier<4>();
-  };
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
@@ -428,22 +420,26 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     }
   };
 
-  // Generic iteration (head and remainder): runtime stage; waits for every
-  // fetch at its end.
-  auto step = [&](int i, bool masked) {
-    if (i + 3 < nb) dma_block(i + 3, (i + 3 - i0) & 3);
-    compute(i, (i - i0) & 3, masked);
+  // Blocks go through the ring in pairs: iteration k computes blocks i = 2k
+  // and i+1 (stages st, st+1) after fetching blocks i+2 and i+3 into the
+  // other two stages, which the previous iteration read, and ends with one
+  // barrier once every fetch has landed. `all`: no range checks (blocks past
+  // the end are fetched as zeros into stages no later iteration reads).
+  auto pair = [&](int i, int st, bool masked, bool all) {
+    if (all || i + 2 < nb) dma_block(i + 2, (st + 2) & 3);
+    if (all || i + 3 < nb) dma_block(i + 3, (st + 3) & 3);
+    compute(i, st, masked);
+    if (all || i + 1 < nb) compute(i + 1, (st + 1) & 3, masked);
     lds_fetch_barrier<0>();
   };
 
-  // Prologue: the workgroup's K and V rows and blocks 0-2 are fetched
-  // straight into LDS (blocks past the end into stages nothing reads); the
-  // first products wait for the K and V rows and block 0 only.
+  // Prologue: the workgroup's K and V rows and blocks 0 and 1 are fetched
+  // straight into LDS (blocks past the end into stages nothing reads).
   dma_rows128(a.K16, head, S, kv_blk0, lds_raw + kOwnOffset);
   dma_rows128(a.V16, head, S, kv_blk0, lds_raw + kOwnOffset + kOwnTile * 2);
-#pragma unroll
-  for (int p = 0; p < 3; ++p) dma_block(p, (p - i0) & 3);
-  fetch_barrier();
+  dma_block(0, (0 - i0) & 3);
+  dma_block(1, (1 - i0) & 3);
+  lds_fetch_barrier<0>();
   {
     // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
     // holds key key0 + c, slots d = 16*ds + 8*hh + j.
@@ -456,22 +452,18 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   }
 
   int i = 0;
-  for (; i < i0 && i < nb; ++i) step(i, true);
-  // Steady state: no mask, every wave active; stage and set are constants
-  // (i - i0 is a multiple of 4 at the top of each trip).
-  auto iter = [&](int ii, auto u) {
-    constexpr int q = decltype(u)::value;
-    dma_block(ii + 3, (q + 3) & 3);
-    compute(ii, q, false);
-    fetch_barrier();
-  };
-  for (; i + 4 <= nb; i += 4) {
-    iter(i, Const<0>{});
-    iter(i + 1, Const<1>{});
-    iter(i + 2, Const<2>{});
-    iter(i + 3, Const<3>{});
+  // Under causal masking blocks 0 and 1 hold the diagonal (stages 2 and 3).
+  if (i0 > 0 && nb > 0) {
+    pair(0, (0 - i0) & 3, true, false);
+    i = 2;
   }
-  for (; i < nb; ++i) step(i, false);
+  // Steady state: no mask, every wave active; the stages are constants
+  // (i - i0 is a multiple of 4 at the top of each trip).
+  for (; i + 4 <= nb; i += 4) {
+    pair(i, 0, false, true);
+    pair(i + 2, 2, false, true);
+  }
+  for (; i < nb; i += 2) pair(i, (i - i0) & 3, false, false);
   // Fetches of blocks past the end may still be landing in the ring, which
   // the exchange below reuses.
   lds_fetch_barrier<0>();
