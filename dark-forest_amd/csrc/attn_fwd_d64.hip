@@ -127,9 +127,11 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
 
   // Per-thread byte offsets within a tile, fixed for the whole loop (the
   // stage adds a constant): K rows (A operand of S^T), V^T slots through
-  // transposed reads (A operand of O^T), the thread's share of a tile store,
-  // and its global float4s.
-  int koff[4], voff[2][2][2], soff[kF4], goff[kF4];
+  // transposed reads (A operand of O^T), the thread's share of a tile store
+  // (one 16-byte granule: row tid/8, granule tid%8) and its two global
+  // float4s (the granule's 8 floats).
+  static_assert(kF4 == 2, "one granule per thread per tile");
+  int koff[4], voff[2][2][2], soff, goff;
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) koff[ds] = 2 * tile_off(kh * 32 + c, 8 * (2 * ds + hh));
 #pragma unroll
@@ -139,12 +141,8 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         voff[j][db][hf] = 2 * tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-#pragma unroll
-  for (int i = 0; i < kF4; ++i) {
-    const int idx = tid + i * kThreads;
-    soff[i] = 2 * tile_off(idx >> 4, (idx & 15) * 4);
-    goff[i] = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
-  }
+  soff = 2 * tile_off(tid >> 3, (tid & 7) * 8);
+  goff = ((tid >> 3) * ld + hoff + (tid & 7) * 8) * 4;
 
   // LDS stages: K tile t in K stage t % 4, V tile t in V stage t % 4.
   auto kstage = [&](int t) { return lds_raw + (t & (kStages - 1)) * kTileBytes; };
@@ -161,11 +159,11 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ld, (unsigned)rows * (unsigned)(ld * 4));
 #pragma unroll
     for (int i = 0; i < kF4; ++i)
-      xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff[i], 0, 0));
+      xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff + 16 * i, 0, 0));
   };
   auto store_rows = [&](unsigned char *dst, const float4 (&xr)[kF4]) {
-#pragma unroll
-    for (int i = 0; i < kF4; ++i) *reinterpret_cast<half4_t *>(dst + soff[i]) = to_half4(xr[i]);
+    const half4_t lo = to_half4(xr[0]), hi = to_half4(xr[1]);
+    *reinterpret_cast<half8_t *>(dst + soff) = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
 
   f32x16 o[2];
