@@ -3,8 +3,11 @@
 
 Workload (the metric's shape): causal scaled-dot-product
 attention forward + backward, fp32 I/O, B=1, H=12, S=4096, D=64, Q/K/V/dO iid
-N(0,1) from fixed seeds, scale 1/8. One step = dfattn_fwd (O, lse) followed by
-dfattn_bwd (its two phases: preprocess, main) on inputs already resident in HBM.
+N(0,1) from fixed seeds, scale 1/8. One step = the training pair: dfattn_fwd_train
+(O, lse, and the backward's fp16 operand copies in the workspace), then the
+backward's two phases (dfattn_bwd_preprocess with DFATTN_BWD_QKV_SAVED, then
+dfattn_bwd_main) on inputs already resident in HBM. `value` is the wall clock of
+exactly `steps` steps between two synchronisations.
 
 FLOPs follow the reference's convention (darkforest-core/src/bin/bench_sequence_limit.rs:226):
 causal forward = 2*H*S^2*D, backward = 2.5x forward, so one step = 7*H*S^2*D
@@ -12,8 +15,11 @@ causal forward = 2*H*S^2*D, backward = 2.5x forward, so one step = 7*H*S^2*D
 
 Prints ONE JSON line. `roofline` is for the dominant kernel (the one with the
 largest average duration, timed live with HIP events on the stream the
-library launches on); `cpu_baseline` times the CPU oracle (a restatement of
-the reference's fp32 CPU attention) on a bounded sample of the same workload.
+library launches on, in a second pass after the timed one; `frac_at_sclk`
+also divides by the peak at the shader clock rocm-smi reports while the step
+runs); `cpu_baseline` times the CPU oracle (a restatement of the reference's
+fp32 CPU attention) on a bounded sample of the same workload on one thread,
+`cpu_baseline_threads` on every head in parallel.
 """
 from __future__ import annotations
 
@@ -64,6 +70,66 @@ def cpu_baseline(heads: int):
             "sample": f"heads 0..{heads - 1} of {H} at S={S}, D={D}: causal fwd+bwd, fp32, 1 thread "
                       f"({dt:.1f} s; {flops / 1e9:.2f} GFLOP algorithmic)",
             "seconds": round(dt, 3)}
+
+
+def cpu_baseline_threads():
+    """The same CPU oracle on all 12 heads, parallel over heads on T = min(cpus, 12) threads."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), H))
+    q, k, v, g = seeded(S, H, D, SEED)
+    t0 = time.perf_counter()
+    O.mha_forward(q, k, v, H, SCALE, True, threads=threads)
+    O.backward(q, k, v, g, H, SCALE, True, threads=threads)
+    dt = time.perf_counter() - t0
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": FLOP_STEP / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"all {H} heads at S={S}, D={D}: causal fwd+bwd, fp32, {threads} threads over heads "
+                      f"({dt:.1f} s)", "seconds": round(dt, 3), "cpus_available": len(os.sched_getaffinity(0)),
+            "cpu_model": model}
+
+
+def sample_sclk(step, seconds=1.5):
+    """Median shader clock (MHz) that rocm-smi reports while `step` runs back to back, or None."""
+    import re
+    import shutil
+    import subprocess
+    import threading
+
+    import torch
+
+    smi = shutil.which("rocm-smi")
+    if smi is None:
+        return None
+    stop = threading.Event()
+
+    def run():
+        while not stop.is_set():
+            for _ in range(20):
+                step()
+            torch.cuda.synchronize()
+
+    th = threading.Thread(target=run)
+    th.start()
+    samples = []
+    try:
+        time.sleep(0.2)
+        t_end = time.time() + seconds
+        while time.time() < t_end:
+            out = subprocess.run([smi, "--showclocks"], capture_output=True, text=True, timeout=20).stdout
+            samples += [int(x) for x in re.findall(r"sclk clock level: \d+: \((\d+)Mhz\)", out)]
+    except (OSError, subprocess.SubprocessError):
+        pass
+    finally:
+        stop.set()
+        th.join()
+    return float(np.median(samples)) if samples else None
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_c2_hbm_traffic.md")
@@ -219,8 +285,8 @@ def seq_limit(max_alloc_s):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-heads", type=int, default=6, help="heads in the CPU baseline sample (0 = skip)")
     ap.add_argument("--gpt2-steps", type=int, default=10,
                     help="timed GPT-2 small training steps at S=1024 (BASELINE configs[4]); 0 = skip")
@@ -284,15 +350,21 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    # The timed region: exactly `steps` steps between two synchronisations, nothing else in it.
     log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
+    for _ in range(args.steps):
+        step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
+    # A second pass with HIP events on the library's stream around every launch gives the
+    # per-kernel durations (the events add their own packets, so they stay out of the timed region).
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
 
     fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     pre_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
@@ -339,6 +411,17 @@ def main():
         "roofline": roofline,
         "gpt2_step_ms": None,
     }
+    # The shader clock the kernels ran at (rocm-smi, sampled while the same step runs back to back
+    # after the timed region) and the roofline fraction against the peak at that clock
+    # (256 CUs x 4096 dense fp16 FLOP/clk/CU).
+    sclk = sample_sclk(step)
+    result["sclk_mhz"] = sclk
+    if sclk:
+        peak_sclk = 256 * 4096 * sclk * 1e6 / 1e12
+        roofline["peak_at_sclk"] = round(peak_sclk, 1)
+        roofline["frac_at_sclk"] = round(roofline["achieved"] / peak_sclk, 4)
+    result["notes"] = ("inputs L2/MALL-warm: the step's ~150 MB of tensors stay resident between steps "
+                       "(the 256 MB Infinity Cache); no flush buffer between steps")
     if args.gpt2_steps > 0:
         from dfattn.gpt2_step import StaticGPT2, time_steps
 
@@ -365,6 +448,8 @@ def main():
     if args.cpu_heads > 0:
         log(f"cpu baseline on {args.cpu_heads} heads")
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+        log("cpu baseline, all heads, parallel over heads")
+        result["cpu_baseline_threads"] = cpu_baseline_threads()
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
