@@ -282,12 +282,10 @@ __device__ __forceinline__ void exchange_pair(float *buf, int wave, int lane, f3
 // kv_blk0 + 32*(w%4) .. +31 and query half w/4 of every 64-row block.
 //
 // Query block i (rows qb0 = 64*(first_qb + i) ..) goes through ring stage
-// (i - i0) % 4 and staging register set (i - i0) % 2, i0 being the number of
-// blocks that hold the causal diagonal (two, or none without masking): in
-// the unrolled steady loop both are compile-time constants. Block i+3 is
-// written into its stage during iteration i (the stage last read in
-// iteration i-1) and block i+5 is fetched into the register set block i+3
-// has just left.
+// (i - i0) % 4, i0 being the number of blocks that hold the causal diagonal
+// (two, or none without masking): in the unrolled steady loop the stage is
+// a compile-time constant. The blocks are fetched straight into LDS and
+// processed in pairs (see `pair` below).
 __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char *lds_raw) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, hh = lane >> 5;
@@ -309,13 +307,12 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int first_qb = a.causal ? kv_blk0 / kQBlock : 0;
   const int nb = max(n_qblocks - first_qb, 0);
   // Under causal masking the first two blocks hold the diagonal of the
-  // workgroup's 128 keys; every later row sees every key. i0 is even, so
-  // block i's register set is i % 2.
+  // workgroup's 128 keys; every later row sees every key.
   const int i0 = a.causal ? 2 : 0;
 
   // Per-thread offsets, fixed for the whole loop: rows qh*32 + c of a tile
   // (A operands of S and dP), this wave's transposed reads (B operands of dV
-  // and dK), the thread's share of the tile stores and its global float4s.
+  // and dK).
   int roff[4], troff[2][2][2];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) roff[ds] = tile_off(qh * 32 + c, 8 * (2 * ds + hh));
@@ -518,12 +515,11 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int n_tiles = (kv_end + kKTile - 1) / kKTile;
   // Tiles below n_full need no mask for any row of the workgroup (causal:
   // every key is below the first row; otherwise every key is below S). They
-  // run first, unrolled by four; the rest take the general loop.
+  // run first, software-pipelined; the rest take the general loop.
   const int n_full = a.causal ? min(q_blk0 / kKTile, n_tiles) : S / kKTile;
 
-  // Per-thread offsets: K/V rows kh*32 + c (A operands of S^T and dP^T), K^T
-  // slots through transposed reads (A operand of dQ^T), tile stores and the
-  // thread's global float4s.
+  // Per-thread offsets: K/V rows kh*32 + c (A operands of S^T and dP^T) and
+  // K^T slots through transposed reads (A operand of dQ^T).
   int koff[4], ktoff[2][2][2];
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds) koff[ds] = tile_off(kh * 32 + c, 8 * (2 * ds + hh));
