@@ -4,6 +4,7 @@
 // Kernel selection: d_head == 64 with 16-byte aligned tensors takes the MFMA
 // kernels (attn_fwd_d64.hip, attn_bwd_d64.hip); every other valid shape takes
 // the exact fp32 kernels in attn_generic.hip. There is no CPU path.
+#include <algorithm>
 #include <climits>
 #include <cstdio>
 #include <cstdlib>
@@ -130,6 +131,68 @@ int legacy_backward(const char *fn, const float *q, const float *k, const float 
     err = dfattn::launch_bwd_generic(q, k, v, d_out, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
                                      (int)d_head, scale, causal != 0, nullptr);
   }
+  return record_hip(err, fn);
+}
+
+// ---- decode --------------------------------------------------------------
+
+// Chunks of the fast decode: enough workgroups to fill the GPU (about 512),
+// at least 256 keys each (one 64-key group per wave).
+constexpr uint32_t kDecodeMinChunk = 256;
+uint32_t decode_chunks(uint32_t n_heads, uint32_t cur_len) {
+  const uint32_t by_len = (cur_len + kDecodeMinChunk - 1) / kDecodeMinChunk;
+  const uint32_t by_grid = (512 + n_heads - 1) / n_heads;
+  return std::max(1u, std::min(by_len, by_grid));
+}
+uint32_t decode_chunk_len(uint32_t cur_len, uint32_t n_chunks) {
+  const uint32_t c = (cur_len + n_chunks - 1) / n_chunks;
+  return (c + 63) / 64 * 64;
+}
+
+// Shared validation of every decode entry point; `table` is checked when
+// `paged`. cur_len == 0 is valid (nothing is computed, as in the reference).
+int check_decode(const char *fn, const float *q, const void *k, const void *v, const int32_t *table,
+                 bool paged, uint32_t page_size, bool bf16, const float *out, uint32_t n_heads,
+                 uint32_t cur_len, uint32_t d_head) {
+  if (n_heads == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": n_heads must be >= 1");
+  if (d_head == 0 || d_head > 128)
+    return record_error(DFATTN_ERR_HEAD_DIM, std::string(fn) + ": d_head must be in the range 1..=128");
+  if (n_heads > kMaxHeads || cur_len > (1u << 30))
+    return record_error(DFATTN_ERR_OVERFLOW, std::string(fn) + ": decode shape is too large");
+  if (paged && page_size == 0)
+    return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": page_size must be >= 1");
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || (paged && table == nullptr))
+    return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  const size_t kv_align = bf16 ? 2 : 4;
+  if (!aligned(q, 4) || !aligned(out, 4) || !aligned(k, kv_align) || !aligned(v, kv_align) ||
+      (paged && !aligned(table, 4)))
+    return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": misaligned pointer");
+  return DFATTN_OK;
+}
+
+bool decode_fast(uint32_t d_head, bool bf16, const float *q, const void *k, const void *v) {
+  const size_t kv_align = bf16 ? 8 : 16;
+  return d_head == 64 && aligned(q, 16) && aligned(k, kv_align) && aligned(v, kv_align);
+}
+
+// The reference's decode launchers: null stream, errors recorded for
+// darkforest_sync. chunk 0 = no split.
+int legacy_decode(const char *fn, const float *q, const void *k, const void *v, const int32_t *table,
+                  bool paged, uint32_t page_size, bool bf16, float *pm, float *pl, float *po, float *out,
+                  uint32_t n_heads, uint32_t cur_len, uint32_t d_head, float scale, uint32_t chunk,
+                  bool splitk) {
+  int st = check_decode(fn, q, k, v, table, paged, page_size, bf16, out, n_heads, cur_len, d_head);
+  if (st != DFATTN_OK) return st;
+  if (splitk && chunk == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": chunk_size must be >= 1");
+  if (cur_len == 0) return DFATTN_OK;
+  // attention_fused.cu:781-784: no split when the keys fit one chunk.
+  const bool split = splitk && cur_len > chunk;
+  if (split && (pm == nullptr || pl == nullptr || po == nullptr))
+    return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null partial buffer");
+  const hipError_t err = dfattn::launch_decode(
+      q, k, v, paged ? table : nullptr, (int)page_size, bf16, out, nullptr, (int)n_heads, (int)cur_len,
+      (int)d_head, scale, split ? (int)chunk : (int)cur_len, split ? pm : nullptr, split ? pl : nullptr,
+      split ? po : nullptr, decode_fast(d_head, bf16, q, k, v), nullptr);
   return record_hip(err, fn);
 }
 
@@ -303,6 +366,95 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v, const float 
     err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
                                      (int)d_head, scale, causal != 0, s);
   return record_hip(err, "attention backward launch");
+}
+
+// ---- decode ----------------------------------------------------------------
+
+void launch_fused_mha_decode_kv(const float *q, const float *k_cache, const float *v_cache, float *out,
+                                uint32_t n_heads, uint32_t cur_seq_len, uint32_t d_head, float scale) {
+  mark_pending_if_failed(legacy_decode("launch_fused_mha_decode_kv", q, k_cache, v_cache, nullptr, false, 1,
+                                       false, nullptr, nullptr, nullptr, out, n_heads, cur_seq_len, d_head,
+                                       scale, 0, false));
+}
+
+void launch_fused_mha_decode_kv_splitk(const float *q, const float *k_cache, const float *v_cache,
+                                       float *partial_m, float *partial_l, float *partial_o, float *out,
+                                       uint32_t n_heads, uint32_t cur_seq_len, uint32_t d_head, float scale,
+                                       uint32_t chunk_size) {
+  mark_pending_if_failed(legacy_decode("launch_fused_mha_decode_kv_splitk", q, k_cache, v_cache, nullptr,
+                                       false, 1, false, partial_m, partial_l, partial_o, out, n_heads,
+                                       cur_seq_len, d_head, scale, chunk_size, true));
+}
+
+void launch_paged_mha_decode_kv(const float *q, const float *k_pool, const float *v_pool,
+                                const int32_t *block_table, float *out, uint32_t n_heads,
+                                uint32_t cur_seq_len, uint32_t d_head, float scale, uint32_t page_size) {
+  mark_pending_if_failed(legacy_decode("launch_paged_mha_decode_kv", q, k_pool, v_pool, block_table, true,
+                                       page_size, false, nullptr, nullptr, nullptr, out, n_heads, cur_seq_len,
+                                       d_head, scale, 0, false));
+}
+
+void launch_paged_mha_decode_kv_splitk(const float *q, const float *k_pool, const float *v_pool,
+                                       const int32_t *block_table, float *partial_m, float *partial_l,
+                                       float *partial_o, float *out, uint32_t n_heads, uint32_t cur_seq_len,
+                                       uint32_t d_head, float scale, uint32_t page_size,
+                                       uint32_t chunk_size) {
+  mark_pending_if_failed(legacy_decode("launch_paged_mha_decode_kv_splitk", q, k_pool, v_pool, block_table,
+                                       true, page_size, false, partial_m, partial_l, partial_o, out, n_heads,
+                                       cur_seq_len, d_head, scale, chunk_size, true));
+}
+
+void launch_paged_mha_decode_kv_bf16(const float *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                                     const int32_t *block_table, float *out, uint32_t n_heads,
+                                     uint32_t cur_seq_len, uint32_t d_head, float scale, uint32_t page_size) {
+  mark_pending_if_failed(legacy_decode("launch_paged_mha_decode_kv_bf16", q, k_pool, v_pool, block_table,
+                                       true, page_size, true, nullptr, nullptr, nullptr, out, n_heads,
+                                       cur_seq_len, d_head, scale, 0, false));
+}
+
+size_t dfattn_decode_workspace_bytes(uint32_t n_heads, uint32_t cur_seq_len, uint32_t d_head) {
+  if (n_heads == 0 || cur_seq_len == 0 || d_head == 0 || d_head > 128 || n_heads > kMaxHeads ||
+      cur_seq_len > (1u << 30))
+    return 0;
+  const uint32_t n_chunks = decode_chunks(n_heads, cur_seq_len);
+  if (n_chunks == 1) return 0;
+  return (size_t)n_heads * n_chunks * (d_head + 2) * sizeof(float);
+}
+
+int dfattn_decode(const float *q, const void *k_cache, const void *v_cache, const int32_t *block_table,
+                  uint32_t page_size, uint32_t kv_dtype, float *out, float *lse, uint32_t n_heads,
+                  uint32_t cur_seq_len, uint32_t d_head, float scale, void *workspace, size_t workspace_bytes,
+                  void *stream) {
+  const char *fn = "dfattn_decode";
+  if (kv_dtype != DFATTN_KV_F32 && kv_dtype != DFATTN_KV_BF16)
+    return record_error(DFATTN_ERR_FLAGS, std::string(fn) + ": unknown kv_dtype");
+  const bool bf16 = kv_dtype == DFATTN_KV_BF16, paged = block_table != nullptr;
+  int st = check_decode(fn, q, k_cache, v_cache, block_table, paged, paged ? page_size : 1, bf16, out, n_heads,
+                        cur_seq_len, d_head);
+  if (st != DFATTN_OK) return st;
+  if (lse != nullptr && !aligned(lse, 4))
+    return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": misaligned pointer");
+  if (cur_seq_len == 0) return DFATTN_OK;
+  const size_t need = dfattn_decode_workspace_bytes(n_heads, cur_seq_len, d_head);
+  if (workspace != nullptr && (workspace_bytes < need || !aligned(workspace, 4)))
+    return record_error(DFATTN_ERR_WORKSPACE, std::string(fn) + ": workspace too small or misaligned");
+  // Without a workspace one workgroup per head walks all keys.
+  const uint32_t n_chunks = workspace != nullptr ? decode_chunks(n_heads, cur_seq_len) : 1;
+  float *pm = nullptr, *pl = nullptr, *po = nullptr;
+  uint32_t chunk = cur_seq_len;
+  if (n_chunks > 1) {
+    chunk = decode_chunk_len(cur_seq_len, n_chunks);
+    const uint32_t used = (cur_seq_len + chunk - 1) / chunk;
+    pm = static_cast<float *>(workspace);
+    pl = pm + (size_t)n_heads * used;
+    po = pl + (size_t)n_heads * used;
+  }
+  const hipError_t err = dfattn::launch_decode(
+      q, k_cache, v_cache, block_table, (int)(paged ? page_size : 1), bf16, out, lse, (int)n_heads,
+      (int)cur_seq_len, (int)d_head, scale, (int)chunk, pm, pl, po,
+      decode_fast(d_head, bf16, q, k_cache, v_cache) && (lse == nullptr || aligned(lse, 4)),
+      static_cast<hipStream_t>(stream));
+  return record_hip(err, "decode launch");
 }
 
 const char *dfattn_status_string(int status) {

@@ -284,4 +284,17 @@ hipError_t launch_bwd_generic(const float *q, const float *k, const float *v,
                               int n_heads, int seq_len, int d_head, float scale, bool causal,
                               hipStream_t stream);
 
+// Single-query decode against a KV cache (attn_decode.hip). k, v: fp32 rows
+// of n_heads*d_head, or bf16 bit patterns (bf16); block_table null for a
+// contiguous cache. chunk >= cur_len or null partials: one workgroup per
+// head writes out (and lse if not null) directly; otherwise the key range is
+// split into ceil(cur_len / chunk) chunks whose partials (part_m, part_l:
+// [n_heads, n_chunks], part_o: [n_heads, n_chunks, d_head]) a second kernel
+// merges. fast: d_head == 64 with 16-byte aligned q and 8-byte aligned
+// cache rows may take the coalesced kernel. cur_len >= 1.
+hipError_t launch_decode(const float *q, const void *k, const void *v, const int32_t *block_table,
+                         int page_size, bool bf16, float *out, float *lse, int n_heads, int cur_len,
+                         int d_head, float scale, int chunk, float *part_m, float *part_l, float *part_o,
+                         bool fast, hipStream_t stream);
+
 }  // namespace dfattn

@@ -52,6 +52,13 @@ SYMBOLS = {
     "dfattn_fwd_train": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "launch_fused_mha_decode_kv": (None, [_P] * 4 + [_U32, _U32, _U32, _F]),
+    "launch_fused_mha_decode_kv_splitk": (None, [_P] * 7 + [_U32, _U32, _U32, _F, _U32]),
+    "launch_paged_mha_decode_kv": (None, [_P] * 5 + [_U32, _U32, _U32, _F, _U32]),
+    "launch_paged_mha_decode_kv_splitk": (None, [_P] * 8 + [_U32, _U32, _U32, _F, _U32, _U32]),
+    "launch_paged_mha_decode_kv_bf16": (None, [_P] * 5 + [_U32, _U32, _U32, _F, _U32]),
+    "dfattn_decode_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
+    "dfattn_decode": (ctypes.c_int, [_P] * 4 + [_U32, _U32, _P, _P, _U32, _U32, _U32, _F, _P, ctypes.c_size_t, _P]),
     "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dfattn_last_error": (ctypes.c_int, []),
     "dfattn_last_error_message": (ctypes.c_char_p, []),
@@ -254,6 +261,84 @@ def launch_attention_backward(q, k, v, d_out, d_q, d_k, d_v, probabilities, seq_
 def darkforest_sync():
     """matmul.cu:21: device synchronize; aborts the process on error."""
     lib().darkforest_sync()
+
+
+# ---------------------------------------------------------------- decode (attention_fused.cu:551-1090)
+KV_F32, KV_BF16 = 0, 1  # DFATTN_KV_F32, DFATTN_KV_BF16
+
+
+def _dev_any(t):
+    """Device pointer of a contiguous CUDA tensor of any dtype (the cache pools: float32 or bf16 bits)."""
+    if t is None:
+        return None
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("dfattn decode takes contiguous device tensors")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def decode_workspace_bytes(n_heads, cur_seq_len, d_head) -> int:
+    return int(lib().dfattn_decode_workspace_bytes(n_heads, cur_seq_len, d_head))
+
+
+def decode(q, k_cache, v_cache, n_heads, cur_seq_len, scale=None, block_table=None, page_size=1, out=None,
+           lse=None, workspace="auto", stream=None):
+    """One query q [H*D] against the first cur_seq_len cached keys. k_cache, v_cache: float32, or bfloat16 /
+    int16 / uint16 (bf16 bit patterns) [rows, H*D]; block_table: int32 pages (None: contiguous).
+    workspace: "auto" allocates dfattn_decode_workspace_bytes, None walks the keys with one workgroup per head.
+    Returns (out [H*D], lse [H])."""
+    torch = _torch()
+    d_head = q.numel() // n_heads
+    if scale is None:
+        scale = d_head ** -0.5
+    kv_dtype = KV_F32 if k_cache.dtype == torch.float32 else KV_BF16
+    if out is None:
+        out = torch.empty(n_heads * d_head, dtype=torch.float32, device=q.device)
+    if lse is None:
+        lse = torch.empty(n_heads, dtype=torch.float32, device=q.device)
+    if isinstance(workspace, str):
+        nbytes = decode_workspace_bytes(n_heads, cur_seq_len, d_head)
+        workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=q.device) if nbytes else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().dfattn_decode(_dev_ptr(q), _dev_any(k_cache), _dev_any(v_cache), _dev_any(block_table),
+                               int(page_size), kv_dtype, _dev_ptr(out), _dev_ptr(lse), n_heads, int(cur_seq_len),
+                               d_head, scale, _dev_any(workspace), ws_bytes, _stream_ptr(stream)))
+    return out, lse
+
+
+def launch_fused_mha_decode_kv(q, k_cache, v_cache, out, n_heads, cur_seq_len, d_head, scale):
+    """attention_fused.cu:617, null stream."""
+    lib().launch_fused_mha_decode_kv(_dev_ptr(q), _dev_ptr(k_cache), _dev_ptr(v_cache), _dev_ptr(out), n_heads,
+                                     cur_seq_len, d_head, scale)
+
+
+def launch_fused_mha_decode_kv_splitk(q, k_cache, v_cache, partial_m, partial_l, partial_o, out, n_heads,
+                                      cur_seq_len, d_head, scale, chunk_size):
+    """attention_fused.cu:762, null stream."""
+    lib().launch_fused_mha_decode_kv_splitk(_dev_ptr(q), _dev_ptr(k_cache), _dev_ptr(v_cache), _dev_ptr(partial_m),
+                                            _dev_ptr(partial_l), _dev_ptr(partial_o), _dev_ptr(out), n_heads,
+                                            cur_seq_len, d_head, scale, chunk_size)
+
+
+def launch_paged_mha_decode_kv(q, k_pool, v_pool, block_table, out, n_heads, cur_seq_len, d_head, scale, page_size):
+    """attention_fused.cu:1028, null stream."""
+    lib().launch_paged_mha_decode_kv(_dev_ptr(q), _dev_ptr(k_pool), _dev_ptr(v_pool), _dev_any(block_table),
+                                     _dev_ptr(out), n_heads, cur_seq_len, d_head, scale, page_size)
+
+
+def launch_paged_mha_decode_kv_splitk(q, k_pool, v_pool, block_table, partial_m, partial_l, partial_o, out,
+                                      n_heads, cur_seq_len, d_head, scale, page_size, chunk_size):
+    """attention_fused.cu:1045, null stream."""
+    lib().launch_paged_mha_decode_kv_splitk(_dev_ptr(q), _dev_ptr(k_pool), _dev_ptr(v_pool), _dev_any(block_table),
+                                            _dev_ptr(partial_m), _dev_ptr(partial_l), _dev_ptr(partial_o),
+                                            _dev_ptr(out), n_heads, cur_seq_len, d_head, scale, page_size,
+                                            chunk_size)
+
+
+def launch_paged_mha_decode_kv_bf16(q, k_pool, v_pool, block_table, out, n_heads, cur_seq_len, d_head, scale,
+                                    page_size):
+    """attention_fused.cu:1075 (bf16 pools as bit patterns), null stream."""
+    lib().launch_paged_mha_decode_kv_bf16(_dev_ptr(q), _dev_any(k_pool), _dev_any(v_pool), _dev_any(block_table),
+                                          _dev_ptr(out), n_heads, cur_seq_len, d_head, scale, page_size)
 
 
 

@@ -58,6 +58,11 @@ typedef enum dfattn_status {
 /* Flags of dfattn_bwd_preprocess. */
 #define DFATTN_BWD_QKV_SAVED 1u /* the workspace holds dfattn_fwd_train's copies */
 
+/* KV-cache element types of dfattn_decode. */
+#define DFATTN_KV_F32 0u  /* fp32 rows                                        */
+#define DFATTN_KV_BF16 1u /* bf16 bit patterns in uint16 (the reference's      */
+                          /* __nv_bfloat16 pools)                             */
+
 /* ---- Group 1: the reference's launcher symbols ---------------------------
  * Same signatures as the reference. Launches go to the legacy default (null)
  * stream; the functions return nothing. Argument errors that the reference
@@ -94,8 +99,54 @@ void launch_fused_mha_backward(const float *q, const float *k, const float *v,
                                uint32_t n_heads, uint32_t seq_len,
                                uint32_t d_head, float scale, uint32_t causal);
 
+/* Decode: one query row q [H*d_head] against the first cur_seq_len rows of a
+ * KV cache, out [H*d_head] (nothing written when cur_seq_len is 0, as the
+ * reference's kernels return early). d_head 1..=128. Contiguous caches are
+ * [max_seq_len, H*d_head]; paged pools are [n_blocks * page_size,
+ * H*d_head] with row t at block_table[t / page_size] * page_size +
+ * t % page_size. The split-K variants take the caller's partial buffers in
+ * the reference's layout (m, l: [H, n_chunks]; o: [H, n_chunks, d_head],
+ * n_chunks = ceil(cur_seq_len / chunk_size)) and, like the reference, do not
+ * split when cur_seq_len <= chunk_size; chunk_size 0 and page_size 0 are
+ * recorded as argument errors (the reference divides by them).             */
+
+/* attention_fused.cu:617 — contiguous fp32 cache.                          */
+void launch_fused_mha_decode_kv(const float *q, const float *k_cache,
+                                const float *v_cache, float *out,
+                                uint32_t n_heads, uint32_t cur_seq_len,
+                                uint32_t d_head, float scale);
+/* attention_fused.cu:762 — contiguous fp32 cache, split over the keys.     */
+void launch_fused_mha_decode_kv_splitk(const float *q, const float *k_cache,
+                                       const float *v_cache, float *partial_m,
+                                       float *partial_l, float *partial_o,
+                                       float *out, uint32_t n_heads,
+                                       uint32_t cur_seq_len, uint32_t d_head,
+                                       float scale, uint32_t chunk_size);
+/* attention_fused.cu:1028 — paged fp32 pool.                               */
+void launch_paged_mha_decode_kv(const float *q, const float *k_pool,
+                                const float *v_pool, const int32_t *block_table,
+                                float *out, uint32_t n_heads,
+                                uint32_t cur_seq_len, uint32_t d_head,
+                                float scale, uint32_t page_size);
+/* attention_fused.cu:1045 — paged fp32 pool, split over the keys.          */
+void launch_paged_mha_decode_kv_splitk(const float *q, const float *k_pool,
+                                       const float *v_pool,
+                                       const int32_t *block_table,
+                                       float *partial_m, float *partial_l,
+                                       float *partial_o, float *out,
+                                       uint32_t n_heads, uint32_t cur_seq_len,
+                                       uint32_t d_head, float scale,
+                                       uint32_t page_size, uint32_t chunk_size);
+/* attention_fused.cu:1075 — paged bf16 pool (bit patterns as uint16).      */
+void launch_paged_mha_decode_kv_bf16(const float *q, const uint16_t *k_pool,
+                                     const uint16_t *v_pool,
+                                     const int32_t *block_table, float *out,
+                                     uint32_t n_heads, uint32_t cur_seq_len,
+                                     uint32_t d_head, float scale,
+                                     uint32_t page_size);
+
 /* matmul.cu:21 — device synchronize; on a HIP error, or on an argument
- * error of one of the four launchers above since the last sync, print
+ * error of one of the launchers above since the last sync, print
  * "[darkforest] ..." to stderr and abort(), as the reference does. Errors
  * the status-returning entry points below already returned do not abort.   */
 void darkforest_sync(void);
@@ -167,6 +218,24 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     float *d_k, float *d_v, void *workspace, size_t workspace_bytes,
                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                     float scale, uint32_t causal, void *stream);
+
+/* Decode on a stream with a status: the five launchers above in one entry
+ * point. block_table NULL: contiguous cache (page_size ignored); kv_dtype
+ * DFATTN_KV_F32 or DFATTN_KV_BF16 (k_cache, v_cache then point to uint16
+ * bf16 bit patterns). lse [H] (natural log of the sum of exp(scale*q.k),
+ * may be NULL) lets callers merge decodes over sharded caches. With a
+ * workspace of dfattn_decode_workspace_bytes the keys are split over enough
+ * workgroups to fill the GPU; with workspace NULL one workgroup per head
+ * walks them all. cur_seq_len 0 returns DFATTN_OK and writes nothing.
+ * Reference counterparts: attention_fused.cu:617, 762, 1028, 1045, 1075
+ * (the reference's launchers have no stream, no status and no lse).       */
+size_t dfattn_decode_workspace_bytes(uint32_t n_heads, uint32_t cur_seq_len,
+                                     uint32_t d_head);
+int dfattn_decode(const float *q, const void *k_cache, const void *v_cache,
+                  const int32_t *block_table, uint32_t page_size,
+                  uint32_t kv_dtype, float *out, float *lse, uint32_t n_heads,
+                  uint32_t cur_seq_len, uint32_t d_head, float scale,
+                  void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- Group 3: the reference's per-layer attention context ---------------
  * Mirror of AttentionContext (darkforest-cuda/src/lib.rs:1949-2368), the

@@ -24,6 +24,9 @@
  *                               measure the fp32 restatement's own error.
  *   oracle_mha_forward_rows_f32 the forward for a chosen set of query rows
  *                               (row-sampled check of S=131072).
+ *   oracle_decode_f32           attention_fused.cu:551-615, 800-866, 968-1033
+ *                               (single-query KV-cache decode: contiguous,
+ *                               paged, bf16 pools), plus its logsumexp.
  *
  * Arithmetic follows the reference: fp32 throughout, sums accumulated
  * sequentially in index order, exp from libm (Rust's f32::exp), mul and add
@@ -328,6 +331,72 @@ void oracle_reference_attention_f32(const float *q, const float *k,
 
 DEFINE_BACKWARD(oracle_reference_backward_f32, float, expf)
 DEFINE_BACKWARD(oracle_backward_f64, double, exp)
+
+/* ------------------------------------------------------------------------
+ * Single-query decode against a KV cache, attention_fused.cu:551-615
+ * (kernel_fused_mha_decode_kv), with the paged addressing of 800-866
+ * (kernel_paged_mha_decode_kv: row t lives in physical block
+ * block_table[t / page_size] at offset t % page_size; pool rows are [d_model])
+ * and the bf16 pools of 968-1033 (each element widened to fp32 exactly).
+ * Per head, over keys t = 0 .. cur_len-1 in order: score = (sum_d q*k) *
+ * scale; m_new = max(m, score); alpha = exp(m - m_new) (0 while m is the
+ * initial -FLT_MAX); p = exp(score - m_new); l = fma(l, alpha, p); o =
+ * fma(p, v, o*alpha) (the reference's fused forms); out = o / l (0 if l is 0). Nothing is written when cur_len is 0, as
+ * the reference's kernels return early. New: lse = m + ln(l) per head (the
+ * natural-log logsumexp of the scores), when lse is not NULL.
+ * q, out: [H*D]; k, v: [cur_len or pool rows, H*D] as float (kv_bf16 = 0) or
+ * as bf16 bit patterns in uint16 (kv_bf16 = 1); block_table NULL means a
+ * contiguous cache.
+ * ---------------------------------------------------------------------- */
+static inline float bf16_to_f32(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+#define DEFINE_DECODE(NAME, T, EXP, LOG, FMA)                                    \
+  void NAME(const T *q, const void *k, const void *v, const int32_t *block_table, \
+            int page_size, int kv_bf16, T *out, T *lse, int n_heads, int cur_len, \
+            int d_head, T scale) {                                               \
+    if (cur_len <= 0) return;                                                    \
+    const size_t dh = (size_t)d_head, dm = (size_t)n_heads * dh;                 \
+    for (int h = 0; h < n_heads; ++h) {                                          \
+      T m = (T)-3.40282346638528859812e+38, l = 0;                               \
+      T *o = out + (size_t)h * dh;                                               \
+      for (size_t d = 0; d < dh; ++d) o[d] = 0;                                  \
+      for (int t = 0; t < cur_len; ++t) {                                        \
+        size_t row = (size_t)t;                                                  \
+        if (block_table)                                                         \
+          row = (size_t)block_table[t / page_size] * (size_t)page_size +         \
+                (size_t)(t % page_size);                                         \
+        const size_t base = row * dm + (size_t)h * dh;                           \
+        T dot = 0;                                                               \
+        for (size_t d = 0; d < dh; ++d) {                                        \
+          const T kval = kv_bf16 ? (T)bf16_to_f32(((const uint16_t *)k)[base + d]) \
+                                 : (T)((const T *)k)[base + d];                  \
+          dot += q[(size_t)h * dh + d] * kval;                                   \
+        }                                                                        \
+        const T score = dot * scale;                                             \
+        const T m_new = score > m ? score : m;                                   \
+        const T alpha = (m == (T)-3.40282346638528859812e+38) ? (T)0 : EXP(m - m_new); \
+        const T p = EXP(score - m_new);                                          \
+        l = FMA(l, alpha, p);                                                    \
+        m = m_new;                                                               \
+        for (size_t d = 0; d < dh; ++d) {                                        \
+          const T vval = kv_bf16 ? (T)bf16_to_f32(((const uint16_t *)v)[base + d]) \
+                                 : (T)((const T *)v)[base + d];                  \
+          o[d] = FMA(p, vval, o[d] * alpha);                                     \
+        }                                                                        \
+      }                                                                          \
+      const T inv_l = l > 0 ? (T)1 / l : (T)0;                                   \
+      for (size_t d = 0; d < dh; ++d) o[d] *= inv_l;                             \
+      if (lse) lse[h] = l > 0 ? m + LOG(l) : (T)-INFINITY;                       \
+    }                                                                            \
+  }
+
+DEFINE_DECODE(oracle_decode_f32, float, expf, logf, fmaf)
+DEFINE_DECODE(oracle_decode_f64, double, exp, log, fma)
 
 /* Number of threads OpenMP would use by default (1 without OpenMP). */
 int oracle_max_threads(void) {

@@ -59,6 +59,10 @@ def _load():
     lib.oracle_reference_attention_f32.argtypes = [f32p, f32p, f32p, f32p, c_int, c_int, c_float, c_int]
     lib.oracle_reference_backward_f32.argtypes = [f32p] * 7 + [c_int, c_int, c_int, c_float, c_int, c_int]
     lib.oracle_backward_f64.argtypes = [f64p] * 7 + [c_int, c_int, c_int, c_double, c_int, c_int]
+    vp, i32p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32)
+    lib.oracle_decode_f32.argtypes = [f32p, vp, vp, i32p, c_int, c_int, f32p, f32p, c_int, c_int, c_int, c_float]
+    lib.oracle_decode_f64.argtypes = [f64p, vp, vp, i32p, c_int, c_int, f64p, f64p, c_int, c_int, c_int, c_double]
+    lib.oracle_decode_f32.restype = lib.oracle_decode_f64.restype = None
     lib.oracle_set_mutation.argtypes = [c_int]
     lib.oracle_get_mutation.restype = c_int
     lib.oracle_max_threads.restype = c_int
@@ -142,6 +146,49 @@ def backward(q, k, v, d_out, n_heads, scale, causal=True, threads=1, dtype=np.fl
     fn(_ptr(q, ct), _ptr(k, ct), _ptr(v, ct), _ptr(d_out, ct), _ptr(dq, ct), _ptr(dk, ct), _ptr(dv, ct),
        n_heads, seq_len, d_head, ct(scale), int(bool(causal)), int(threads))
     return dq, dk, dv
+
+
+def decode(q, k_cache, v_cache, n_heads, cur_len, scale, block_table=None, page_size=1, dtype=np.float32):
+    """Single-query KV-cache decode (attention_fused.cu:551-615; paged 800-866; bf16 968-1033).
+
+    q: [H*D]. k_cache, v_cache: [rows, H*D] float (fp32, or fp64 with dtype) or uint16 bf16 bit
+    patterns. block_table: int32 logical page -> physical block (None: contiguous cache).
+    Returns (out [H*D], lse [H]); cur_len = 0 returns (None, None) as nothing is computed.
+    """
+    lib = _load()
+    ct = ctypes.c_float if dtype == np.float32 else ctypes.c_double
+    q = _as(q, dtype).reshape(-1)
+    bf16 = np.asarray(k_cache).dtype == np.uint16
+    if bf16:
+        k_cache, v_cache = (np.ascontiguousarray(a, dtype=np.uint16) for a in (k_cache, v_cache))
+    else:
+        k_cache, v_cache = _as(k_cache, dtype), _as(v_cache, dtype)
+    d_head = q.size // n_heads
+    out = np.full(q.size, np.nan, dtype=dtype)
+    lse = np.full(n_heads, np.nan, dtype=dtype)
+    if block_table is not None:
+        block_table = np.ascontiguousarray(block_table, dtype=np.int32)
+        bt = block_table.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    else:
+        bt = None
+    fn = lib.oracle_decode_f32 if dtype == np.float32 else lib.oracle_decode_f64
+    fn(_ptr(q, ct), k_cache.ctypes.data_as(ctypes.c_void_p), v_cache.ctypes.data_as(ctypes.c_void_p), bt,
+       int(page_size), int(bf16), _ptr(out, ct), _ptr(lse, ct), n_heads, int(cur_len), d_head, ct(scale))
+    if cur_len <= 0:
+        return None, None
+    return out, lse
+
+
+def to_bf16_bits(a):
+    """fp32 -> bf16 bit patterns (round to nearest even), as uint16."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def from_bf16_bits(b):
+    """bf16 bit patterns (uint16) -> fp32, exactly."""
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 def seeded_inputs(seq_len, n_heads, d_head, seed, std=1.0, with_grad=True):

@@ -183,3 +183,49 @@ def test_context_error_is_returned_and_recorded_in_a_fresh_process():
             "assert lib.dfattn_last_error() == -4; print('ok')") % os.path.join(ROOT, "dark-forest_amd")
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and "ok" in out.stdout, out.stderr
+
+
+# ---------------------------------------------------------------- decode (attention_fused.cu:551-1090)
+def dec(q=FAKE, k=FAKE, v=FAKE, table=None, page=1, kvt=0, out=FAKE, lse=None, h=12, n=100, d=64, ws=None,
+        wsb=0):
+    return dfattn.lib().dfattn_decode(q, k, v, table, page, kvt, out, lse, h, n, d, 0.125, ws, wsb, None)
+
+
+@pytest.mark.parametrize("kwargs,status", [
+    (dict(kvt=2), -8), (dict(d=0), -4), (dict(d=129), -4), (dict(h=0), -3), (dict(h=65536), -5),
+    (dict(q=None), -1), (dict(out=None), -1), (dict(k=ODD), -2), (dict(table=FAKE, page=0), -3),
+    (dict(ws=FAKE, wsb=8, n=4096), -6),
+])
+def test_decode_validation(kwargs, status):
+    """Every case fails on the host before any launch (the pointers are fake)."""
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    assert dec(**kwargs) == status
+    assert lib.dfattn_last_error() == status
+    lib.dfattn_clear_error()
+
+
+def test_decode_empty_cache_is_a_no_op():
+    # cur_seq_len 0: nothing to compute, nothing launched (the reference's kernels return early).
+    assert dec(n=0) == 0
+
+
+def test_decode_workspace_formula():
+    lib = dfattn.lib()
+    # chunks = min(ceil(L/256), ceil(512/H)); one chunk needs no workspace; else H*chunks*(D+2) floats
+    assert lib.dfattn_decode_workspace_bytes(12, 256, 64) == 0
+    assert lib.dfattn_decode_workspace_bytes(12, 4096, 64) == 12 * 16 * 66 * 4
+    assert lib.dfattn_decode_workspace_bytes(12, 131072, 64) == 12 * 43 * 66 * 4
+    assert lib.dfattn_decode_workspace_bytes(0, 100, 64) == 0
+
+
+def test_legacy_decode_split_with_zero_chunk_is_recorded():
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    # the reference divides by chunk_size (attention_fused.cu:786); here it is an argument error
+    lib.launch_fused_mha_decode_kv_splitk(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 12, 100, 64, 0.1, 0)
+    assert lib.dfattn_last_error() == -3
+    lib.dfattn_clear_error()
+    lib.launch_paged_mha_decode_kv(FAKE, FAKE, FAKE, FAKE, FAKE, 12, 100, 64, 0.1, 0)
+    assert lib.dfattn_last_error() == -3
+    lib.dfattn_clear_error()

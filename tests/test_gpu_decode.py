@@ -1,0 +1,161 @@
+"""GPU parity of the KV-cache decode family (attention_fused.cu:551-1090) against the CPU oracle.
+
+Decode is fp32 arithmetic end to end (the cache is read as fp32, or as bf16 widened exactly), so the
+bar is tight: max-abs <= 2e-5 and relative L2 <= 1e-5 against oracle.decode, itself pinned to the
+causal forward's last row, to float64 SDPA, and paged == contiguous (tests/test_oracle.py).
+"""
+import numpy as np
+import pytest
+
+import dfattn
+import oracle as O
+from test_gpu_parity import host, say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-5, 1e-5
+
+
+def close(name, got, want):
+    ea = float(np.max(np.abs(got - want)))
+    er = float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+    assert np.all(np.isfinite(got)), f"{name}: non-finite"
+    assert ea <= MAX_ABS and er <= REL_L2, f"{name}: max-abs {ea:.2e}, rel-L2 {er:.2e}"
+    return ea, er
+
+
+def cache(rows, n_heads, d_head, seed):
+    x = O.seeded_inputs(rows, n_heads, d_head, seed, with_grad=False)
+    return x["q"][rows - 1].copy(), x["k"], x["v"]
+
+
+def paged_pool(rows_k, rows_v, page_size, seed):
+    n = rows_k.shape[0]
+    n_pages = (n + page_size - 1) // page_size
+    spare = 3
+    perm = np.random.default_rng(seed).permutation(n_pages + spare)[:n_pages].astype(np.int32)
+    shape = ((n_pages + spare) * page_size, rows_k.shape[1])
+    fill = np.random.default_rng(seed + 1)
+    pk = fill.standard_normal(shape).astype(rows_k.dtype) if rows_k.dtype != np.uint16 else np.zeros(shape, np.uint16)
+    pv = fill.standard_normal(shape).astype(rows_v.dtype) if rows_v.dtype != np.uint16 else np.zeros(shape, np.uint16)
+    for lp in range(n_pages):
+        m = min(page_size, n - lp * page_size)
+        pk[perm[lp] * page_size: perm[lp] * page_size + m] = rows_k[lp * page_size: lp * page_size + m]
+        pv[perm[lp] * page_size: perm[lp] * page_size + m] = rows_v[lp * page_size: lp * page_size + m]
+    return pk, pv, perm
+
+
+def dev_any(a, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+@pytest.mark.parametrize("cur_len", [1, 5, 63, 64, 65, 255, 256, 257, 1000, 4096])
+@pytest.mark.parametrize("split", [True, False])
+def test_decode_contiguous_d64(device, cur_len, split):
+    H, D, scale = 12, 64, 0.125
+    say(f"decode contiguous H={H} D={D} L={cur_len} split={split}")
+    q, k, v = cache(cur_len + 7, H, D, 8000 + cur_len)  # cache longer than the live rows
+    want, want_lse = O.decode(q, k, v, H, cur_len, scale)
+    out, lse = dfattn.decode(to_dev(q, device), to_dev(k, device), to_dev(v, device), H, cur_len, scale,
+                             workspace="auto" if split else None)
+    close(f"L={cur_len} out", host(out), want)
+    close(f"L={cur_len} lse", host(lse), want_lse)
+
+
+@pytest.mark.parametrize("d_head", [3, 32, 100, 128])
+def test_decode_generic_head_dims(device, d_head):
+    H, L, scale = 4, 300, d_head ** -0.5
+    say(f"decode generic D={d_head} L={L}")
+    q, k, v = cache(L, H, d_head, 8100 + d_head)
+    want, want_lse = O.decode(q, k, v, H, L, scale)
+    for ws in ("auto", None):
+        out, lse = dfattn.decode(to_dev(q, device), to_dev(k, device), to_dev(v, device), H, L, scale, workspace=ws)
+        close(f"D={d_head} out", host(out), want)
+        close(f"D={d_head} lse", host(lse), want_lse)
+
+
+@pytest.mark.parametrize("page_size,cur_len", [(1, 70), (16, 1000), (64, 4096), (7, 257)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_decode_paged(device, page_size, cur_len, bf16):
+    H, D, scale = 12, 64, 0.125
+    say(f"decode paged page={page_size} L={cur_len} bf16={bf16}")
+    q, k, v = cache(cur_len, H, D, 8200 + cur_len)
+    if bf16:
+        k, v = O.to_bf16_bits(k), O.to_bf16_bits(v)
+    pk, pv, table = paged_pool(k, v, page_size, 8300 + page_size)
+    want, want_lse = O.decode(q, pk, pv, H, cur_len, scale, block_table=table, page_size=page_size)
+    for ws in ("auto", None):
+        out, lse = dfattn.decode(to_dev(q, device), dev_any(pk.view(np.int16) if bf16 else pk, device),
+                                 dev_any(pv.view(np.int16) if bf16 else pv, device), H, cur_len, scale,
+                                 block_table=dev_any(table, device), page_size=page_size, workspace=ws)
+        close(f"paged {page_size} out", host(out), want)
+        close(f"paged {page_size} lse", host(lse), want_lse)
+
+
+@pytest.mark.parametrize("cur_len,chunk", [(100, 128), (1000, 128), (4096, 1000), (300, 7)])
+def test_reference_launchers(device, cur_len, chunk):
+    """The five reference symbols (null stream), the split-K ones with the caller's partial buffers."""
+    import torch
+
+    H, D, scale = 12, 64, 0.125
+    say(f"decode reference launchers L={cur_len} chunk={chunk}")
+    q, k, v = cache(cur_len, H, D, 8400 + cur_len)
+    want, _ = O.decode(q, k, v, H, cur_len, scale)
+    dq, dk, dv = to_dev(q, device), to_dev(k, device), to_dev(v, device)
+    n_chunks = (cur_len + chunk - 1) // chunk
+    pm = torch.empty(H * n_chunks, device=device)
+    pl = torch.empty_like(pm)
+    po = torch.empty(H * n_chunks * D, device=device)
+    out = torch.full((H * D,), float("nan"), device=device)
+    dfattn.launch_fused_mha_decode_kv(dq, dk, dv, out, H, cur_len, D, scale)
+    dfattn.darkforest_sync()
+    close("decode_kv", host(out), want)
+    out.fill_(float("nan"))
+    dfattn.launch_fused_mha_decode_kv_splitk(dq, dk, dv, pm, pl, po, out, H, cur_len, D, scale, chunk)
+    dfattn.darkforest_sync()
+    close("decode_kv_splitk", host(out), want)
+    page = 16
+    pk, pv, table = paged_pool(k, v, page, 8500)
+    dpk, dpv, dtab = dev_any(pk, device), dev_any(pv, device), dev_any(table, device)
+    out.fill_(float("nan"))
+    dfattn.launch_paged_mha_decode_kv(dq, dpk, dpv, dtab, out, H, cur_len, D, scale, page)
+    dfattn.darkforest_sync()
+    close("paged", host(out), want)
+    out.fill_(float("nan"))
+    dfattn.launch_paged_mha_decode_kv_splitk(dq, dpk, dpv, dtab, pm, pl, po, out, H, cur_len, D, scale, page, chunk)
+    dfattn.darkforest_sync()
+    close("paged_splitk", host(out), want)
+    kb, vb = O.to_bf16_bits(pk), O.to_bf16_bits(pv)
+    want_bf, _ = O.decode(q, kb, vb, H, cur_len, scale, block_table=table, page_size=page)
+    out.fill_(float("nan"))
+    dfattn.launch_paged_mha_decode_kv_bf16(dq, dev_any(kb.view(np.int16), device), dev_any(vb.view(np.int16), device),
+                                           dtab, out, H, cur_len, D, scale, page)
+    dfattn.darkforest_sync()
+    close("paged_bf16", host(out), want_bf)
+
+
+def test_empty_cache_writes_nothing(device):
+    import torch
+
+    H, D = 12, 64
+    q, k, v = cache(10, H, D, 8600)
+    out = torch.full((H * D,), 7.0, device=device)
+    dfattn.launch_fused_mha_decode_kv(to_dev(q, device), to_dev(k, device), to_dev(v, device), out, H, 0, D, 0.125)
+    dfattn.darkforest_sync()
+    out2, _ = dfattn.decode(to_dev(q, device), to_dev(k, device), to_dev(v, device), H, 0, 0.125, out=out.clone())
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all()) and bool((out2 == 7.0).all())
+
+
+def test_decode_is_the_forward_last_row_on_gpu(device):
+    """The decode of query i equals row i of the GPU's own causal forward (fp16 operands there)."""
+    H, D, L = 12, 64, 512
+    x = O.seeded_inputs(L, H, D, 8700, with_grad=False)
+    o, lse = dfattn.attention_forward(to_dev(x["q"], device), to_dev(x["k"], device), to_dev(x["v"], device), H,
+                                      0.125, True)
+    out, dlse = dfattn.decode(to_dev(x["q"][L - 1], device), to_dev(x["k"], device), to_dev(x["v"], device), H, L,
+                              0.125)
+    assert np.abs(host(out) - host(o)[L - 1]).max() < 2e-3
+    assert np.abs(host(dlse) - host(lse)[:, L - 1]).max() < 2e-3

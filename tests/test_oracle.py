@@ -266,3 +266,78 @@ def test_seeded_inputs_are_reproducible():
     assert all(np.array_equal(a[n], b[n]) for n in a)
     assert not np.array_equal(a["q"], a["k"])
     assert math.isclose(float(O.seeded_inputs(4096, 1, 64, 1, with_grad=False)["q"].std()), 1.0, rel_tol=0.02)
+
+
+# ---------------------------------------------------------------- decode (attention_fused.cu:551-1033)
+def _paged_pool(rows, page_size, seed):
+    """Scatter `rows` into a pool of pages in a random physical order; returns (pool, block_table)."""
+    n = rows.shape[0]
+    n_pages = (n + page_size - 1) // page_size
+    perm = np.random.default_rng(seed).permutation(n_pages + 3)[:n_pages].astype(np.int32)
+    pool = np.random.default_rng(seed + 1).standard_normal(((n_pages + 3) * page_size, rows.shape[1])).astype(
+        rows.dtype) if rows.dtype != np.uint16 else np.zeros(((n_pages + 3) * page_size, rows.shape[1]), np.uint16)
+    for lp in range(n_pages):
+        m = min(page_size, n - lp * page_size)
+        pool[perm[lp] * page_size: perm[lp] * page_size + m] = rows[lp * page_size: lp * page_size + m]
+    return pool, perm
+
+
+@pytest.mark.parametrize("cur_len", [1, 2, 63, 64, 65, 300])
+def test_decode_is_the_causal_forward_of_the_last_row(cur_len):
+    """Decode of query i over keys 0..i is row i of the (separately pinned) causal forward."""
+    H, D = 4, 64
+    x = O.seeded_inputs(cur_len, H, D, 7100 + cur_len, with_grad=False)
+    o, lse = O.mha_forward(x["q"], x["k"], x["v"], H, 0.125, True, dtype=np.float64)
+    i = cur_len - 1
+    d64, l64 = O.decode(x["q"][i], x["k"], x["v"], H, cur_len, 0.125, dtype=np.float64)
+    assert np.abs(d64 - o[i]).max() < 1e-12 and np.abs(l64 - lse[:, i]).max() < 1e-12
+    d32, l32 = O.decode(x["q"][i], x["k"], x["v"], H, cur_len, 0.125)
+    assert np.abs(d32 - o[i]).max() < 2e-6 and np.abs(l32 - lse[:, i]).max() < 2e-6
+
+
+def test_decode_matches_torch_float64_sdpa():
+    torch = pytest.importorskip("torch")
+    H, D, S = 3, 32, 77
+    x = O.seeded_inputs(S, H, D, 7200, with_grad=False)
+    q = torch.from_numpy(x["q"][S - 1].astype(np.float64)).view(1, H, 1, D)
+    k = torch.from_numpy(x["k"].astype(np.float64)).view(S, H, D).permute(1, 0, 2).unsqueeze(0)
+    v = torch.from_numpy(x["v"].astype(np.float64)).view(S, H, D).permute(1, 0, 2).unsqueeze(0)
+    want = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=0.2).reshape(-1).numpy()
+    got, _ = O.decode(x["q"][S - 1], x["k"], x["v"], H, S, 0.2, dtype=np.float64)
+    assert np.abs(got - want).max() < 1e-12
+
+
+@pytest.mark.parametrize("page_size", [1, 7, 16])
+def test_decode_paged_equals_contiguous(page_size):
+    H, D, S = 2, 64, 100
+    x = O.seeded_inputs(S, H, D, 7300, with_grad=False)
+    pk, table = _paged_pool(x["k"], page_size, 1)
+    pv, table_v = _paged_pool(x["v"], page_size, 1)
+    assert np.array_equal(table, table_v)
+    want = O.decode(x["q"][5], x["k"], x["v"], H, S, 0.125)
+    got = O.decode(x["q"][5], pk, pv, H, S, 0.125, block_table=table, page_size=page_size)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_decode_bf16_pool_is_the_widened_values():
+    H, D, S = 2, 64, 90
+    x = O.seeded_inputs(S, H, D, 7400, with_grad=False)
+    kb, vb = O.to_bf16_bits(x["k"]), O.to_bf16_bits(x["v"])
+    # bf16 conversion round trip is exact for values already representable, and rounds to nearest
+    assert np.array_equal(O.to_bf16_bits(O.from_bf16_bits(kb)), kb)
+    assert np.abs(O.from_bf16_bits(kb) - x["k"]).max() <= np.abs(x["k"]).max() * 2.0 ** -8
+    got = O.decode(x["q"][0], kb, vb, H, S, 0.125)
+    want = O.decode(x["q"][0], O.from_bf16_bits(kb), O.from_bf16_bits(vb), H, S, 0.125)
+    assert np.array_equal(got[0], want[0])
+
+
+def test_decode_closed_forms():
+    H, D, S = 2, 16, 40
+    x = O.seeded_inputs(S, H, D, 7500, with_grad=False)
+    out, lse = O.decode(x["q"][0], x["k"], x["v"], H, 1, 0.5)
+    assert np.array_equal(out, x["v"][0])  # one key: P = 1
+    qk = (x["q"][0].reshape(H, D).astype(np.float64) * x["k"][0].reshape(H, D)).sum(1) * 0.5
+    assert np.abs(lse - qk).max() < 1e-5
+    out, lse = O.decode(np.zeros(H * D, np.float32), x["k"], x["v"], H, S, 0.5)  # q = 0: the mean of V
+    assert np.abs(out - x["v"].mean(0)).max() < 1e-5 and np.abs(lse - math.log(S)).max() < 1e-5
+    assert O.decode(x["q"][0], x["k"], x["v"], H, 0, 0.5) == (None, None)  # nothing computed
