@@ -226,6 +226,67 @@ def summarize_trace(stats_csv):
 SEQ_LIMIT_LENGTHS = (8192, 16384, 32768, 65536, 131072, 262144, 524288, 1048576, 2097152)
 
 
+DECODE_CONFIGS = (  # (cache rows L, kv dtype, page size or 0 for a contiguous cache)
+    (1024, "f32", 0),      # GPT-2 small decode at S=1024 (static_gpt2.rs:775-884)
+    (4096, "f32", 0),
+    (131072, "f32", 0),    # C3's context length
+    (131072, "bf16", 16),  # paged bf16 pool (attention_fused.cu:968-1090)
+)
+
+
+def decode_bench(repeats=50):
+    """Single-query decode (dfattn_decode with its workspace), H=12, D=64: the average call time over
+    `repeats` back-to-back calls between HIP events, and the bandwidth of the bytes the call must read
+    (K and V rows of every head, plus q and out) against MI355X's 8 TB/s HBM peak. The caches are the
+    same between calls, so the shorter ones are partly L2/MALL-resident."""
+    import torch
+
+    import dfattn
+
+    dev = torch.device("cuda:0")
+    h, d = 12, 64
+    rows = []
+    for L, kv, page in DECODE_CONFIGS:
+        gen = torch.Generator(device=dev).manual_seed(5000 + L)
+        q = torch.randn(h * d, generator=gen, device=dev)
+        k = torch.randn(L, h * d, generator=gen, device=dev)
+        v = torch.randn(L, h * d, generator=gen, device=dev)
+        elem = 4
+        if kv == "bf16":
+            k, v = (t.to(torch.bfloat16).view(torch.int16) for t in (k, v))
+            elem = 2
+        table = None
+        if page:
+            n_pages = (L + page - 1) // page
+            table = torch.randperm(n_pages, generator=torch.Generator().manual_seed(7), dtype=torch.int32).to(dev)
+        out = torch.empty(h * d, device=dev)
+        lse = torch.empty(h, device=dev)
+        nbytes = dfattn.decode_workspace_bytes(h, L, d)
+        ws = torch.empty(max(nbytes // 4, 1), device=dev) if nbytes else None
+
+        def call():
+            dfattn.decode(q, k, v, h, L, 0.125, block_table=table, page_size=page or 1, out=out, lse=lse,
+                          workspace=ws)
+
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(repeats):
+            call()
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) / repeats * 1e3
+        moved = 2 * L * h * d * elem + 2 * h * d * 4
+        gbps = moved / (us * 1e-6) / 1e9
+        rows.append({"cache_rows": L, "kv": kv, "paged": bool(page), "page_size": page or None, "us": round(us, 2),
+                     "bytes": moved, "GB_per_s": round(gbps, 1), "frac_hbm": round(gbps / 8000.0, 4)})
+        del q, k, v, table, ws
+        torch.cuda.empty_cache()
+    return rows
+
+
 def seq_limit(max_alloc_s):
     """Forward-only sequence-length sweep (darkforest-core/src/bin/bench_sequence_limit.rs:37-335).
 
@@ -299,6 +360,7 @@ def main():
                     help="print a rocprofv3 --kernel-trace --stats summary table and exit (no GPU)")
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
+    ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
     ap.add_argument("--seq-limit", type=int, default=0, metavar="MAX_S",
                     help="run the reference's forward sequence-length sweep up to MAX_S instead of the C2 bench")
     args = ap.parse_args()
@@ -422,6 +484,11 @@ def main():
         roofline["frac_at_sclk"] = round(roofline["achieved"] / peak_sclk, 4)
     result["notes"] = ("inputs L2/MALL-warm: the step's ~150 MB of tensors stay resident between steps "
                        "(the 256 MB Infinity Cache); no flush buffer between steps")
+    if args.decode:
+        log("decode (KV cache, one query row per head)")
+        result["decode"] = {"config": "H=12, D=64, one query; dfattn_decode with its workspace; bytes = K and V "
+                                      "rows of every head + q + out; peak 8 TB/s",
+                            "rows": decode_bench()}
     if args.gpt2_steps > 0:
         from dfattn.gpt2_step import StaticGPT2, time_steps
 

@@ -14,7 +14,7 @@
 // decode_reduce_kernel merges with the logsumexp identity.
 //
 // decode_d64_kernel (D = 64, the GPT-2 shape; fp32 or bf16 cache, contiguous
-// or paged): 4 waves; each wave takes 64-key groups. Its loads are coalesced
+// or paged): 8 waves; each wave takes 64-key groups. Its loads are coalesced
 // rows: lane l reads 4 values (16 bytes fp32, 8 bytes bf16) of row
 // 4j + l/16 of the group at column 4*(l%16), for j = 0..15, K and V alike.
 // The score of a row is reduced over its 16 lanes, gathered through LDS so
@@ -29,7 +29,7 @@ namespace dfattn {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kDecWaves = 4;
+constexpr int kDecWaves = 8;
 constexpr int kDecThreads = 64 * kDecWaves;
 
 struct DecodeArgs {
@@ -53,16 +53,36 @@ __device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {
   return __builtin_bit_cast(float, (unsigned)b << 16);
 }
 
-// 4 consecutive values of a cache row as fp32.
+// 4 consecutive values of a cache row: the raw bits (fp32: the floats; bf16:
+// four bf16 in the low 8 bytes), loaded without conversion so that every
+// load of a group is issued before the first wait, and widened later.
 template <bool BF16>
-__device__ __forceinline__ float4 load4(const void *base, size_t elem) {
+__device__ __forceinline__ uint4 load4_raw(const void *base, size_t elem) {
   if constexpr (BF16) {
     const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const unsigned short *>(base) + elem);
-    return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
-                       __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u));
+    return make_uint4(u.x, u.y, 0u, 0u);
   } else {
-    return *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(base) + elem);
+    return *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(base) + elem);
   }
+}
+template <bool BF16>
+__device__ __forceinline__ float4 widen4(uint4 r) {
+  if constexpr (BF16)
+    return make_float4(__builtin_bit_cast(float, r.x << 16), __builtin_bit_cast(float, r.x & 0xffff0000u),
+                       __builtin_bit_cast(float, r.y << 16), __builtin_bit_cast(float, r.y & 0xffff0000u));
+  else
+    return __builtin_bit_cast(float4, r);
+}
+
+// Sum over each row of 16 lanes, in every lane of the row: DPP rotations
+// within the row (row_ror:8, 4, 2, 1), full-rate VALU instead of LDS-pipe
+// permutes.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+  return x;
 }
 
 template <bool BF16>
@@ -116,24 +136,21 @@ __global__ __launch_bounds__(kDecThreads) void decode_d64_kernel(DecodeArgs a) {
       row_lds[wave][lane] = (unsigned)cache_row(a, t);
       __builtin_amdgcn_wave_barrier();
     }
-    float4 kr[16], vr[16];
+    // Rows past t1 read row t1-1 instead (their P is 0), so every load is
+    // unconditional.
+    uint4 kr[16], vr[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int t = g0 + 4 * j + sub;
-      if (t < t1) {
-        const size_t row = PAGED ? (size_t)row_lds[wave][4 * j + sub] : (size_t)t;
-        const size_t e = row * dm + col;
-        kr[j] = load4<BF16>(a.k, e);
-        vr[j] = load4<BF16>(a.v, e);
-      } else {
-        kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      const int t = min(g0 + 4 * j + sub, t1 - 1);
+      const size_t row = PAGED ? (size_t)row_lds[wave][min(4 * j + sub, t1 - 1 - g0)] : (size_t)t;
+      const size_t e = row * dm + col;
+      kr[j] = load4_raw<BF16>(a.k, e);
+      vr[j] = load4_raw<BF16>(a.v, e);
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      float s = q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off, 64);
+      const float4 k4 = widen4<BF16>(kr[j]);
+      const float s = row16_sum(q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w);
       if (dq == 0) s_lds[wave][4 * j + sub] = s;
     }
     __builtin_amdgcn_wave_barrier();
@@ -155,10 +172,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_d64_kernel(DecodeArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float pj = s_lds[wave][4 * j + sub];
-      o4.x += pj * vr[j].x;
-      o4.y += pj * vr[j].y;
-      o4.z += pj * vr[j].z;
-      o4.w += pj * vr[j].w;
+      const float4 v4 = widen4<BF16>(vr[j]);
+      o4.x += pj * v4.x;
+      o4.y += pj * v4.y;
+      o4.z += pj * v4.z;
+      o4.w += pj * v4.w;
     }
     __builtin_amdgcn_wave_barrier();
   }

@@ -137,9 +137,11 @@ int legacy_backward(const char *fn, const float *q, const float *k, const float 
 // ---- decode --------------------------------------------------------------
 
 // Chunks of the fast decode: enough workgroups to fill the GPU (about 512),
-// at least 256 keys each (one 64-key group per wave).
-constexpr uint32_t kDecodeMinChunk = 256;
+// at least 512 keys each (one 64-key group per wave); up to 1024 keys the
+// second launch costs more than one workgroup per head takes.
+constexpr uint32_t kDecodeMinChunk = 512;
 uint32_t decode_chunks(uint32_t n_heads, uint32_t cur_len) {
+  if (cur_len <= 1024) return 1;
   const uint32_t by_len = (cur_len + kDecodeMinChunk - 1) / kDecodeMinChunk;
   const uint32_t by_grid = (512 + n_heads - 1) / n_heads;
   return std::max(1u, std::min(by_len, by_grid));

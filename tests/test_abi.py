@@ -212,9 +212,10 @@ def test_decode_empty_cache_is_a_no_op():
 
 def test_decode_workspace_formula():
     lib = dfattn.lib()
-    # chunks = min(ceil(L/256), ceil(512/H)); one chunk needs no workspace; else H*chunks*(D+2) floats
-    assert lib.dfattn_decode_workspace_bytes(12, 256, 64) == 0
-    assert lib.dfattn_decode_workspace_bytes(12, 4096, 64) == 12 * 16 * 66 * 4
+    # chunks = min(ceil(L/512), ceil(512/H)), 1 up to L = 1024; one chunk needs no workspace; else
+    # H*chunks*(D+2) floats
+    assert lib.dfattn_decode_workspace_bytes(12, 1024, 64) == 0
+    assert lib.dfattn_decode_workspace_bytes(12, 4096, 64) == 12 * 8 * 66 * 4
     assert lib.dfattn_decode_workspace_bytes(12, 131072, 64) == 12 * 43 * 66 * 4
     assert lib.dfattn_decode_workspace_bytes(0, 100, 64) == 0
 
