@@ -137,7 +137,17 @@ KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_convert_kernel", "bwd
 
 
 def short_kernel_name(name):
+    import re
+
     for k in KERNELS + ("copyBuffer",):
+        if k in name:
+            return k
+    m = re.search(r"decode_d64_kernel(?:ILb([01])ELb([01])E|<(true|false), (true|false)>)", name)
+    if m:
+        bf16 = m.group(1) == "1" or m.group(3) == "true"
+        paged = m.group(2) == "1" or m.group(4) == "true"
+        return f"decode_d64_kernel<{'bf16' if bf16 else 'f32'}, {'paged' if paged else 'contiguous'}>"
+    for k in ("decode_reduce_kernel", "decode_generic_kernel"):
         if k in name:
             return k
     return None
@@ -234,7 +244,7 @@ DECODE_CONFIGS = (  # (cache rows L, kv dtype, page size or 0 for a contiguous c
 )
 
 
-def decode_bench(repeats=50):
+def decode_bench(repeats=50, configs=DECODE_CONFIGS):
     """Single-query decode (dfattn_decode with its workspace), H=12, D=64: the average call time over
     `repeats` back-to-back calls between HIP events, and the bandwidth of the bytes the call must read
     (K and V rows of every head, plus q and out) against MI355X's 8 TB/s HBM peak. The caches are the
@@ -246,7 +256,7 @@ def decode_bench(repeats=50):
     dev = torch.device("cuda:0")
     h, d = 12, 64
     rows = []
-    for L, kv, page in DECODE_CONFIGS:
+    for L, kv, page in configs:
         gen = torch.Generator(device=dev).manual_seed(5000 + L)
         q = torch.randn(h * d, generator=gen, device=dev)
         k = torch.randn(L, h * d, generator=gen, device=dev)
@@ -361,9 +371,14 @@ def main():
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
+    ap.add_argument("--decode-only", type=int, default=-1, metavar="I",
+                    help="time only DECODE_CONFIGS[I] (200 calls) and print its row (for rocprofv3)")
     ap.add_argument("--seq-limit", type=int, default=0, metavar="MAX_S",
                     help="run the reference's forward sequence-length sweep up to MAX_S instead of the C2 bench")
     args = ap.parse_args()
+    if args.decode_only >= 0:
+        print(json.dumps(decode_bench(repeats=200, configs=(DECODE_CONFIGS[args.decode_only],))[0]), flush=True)
+        return
     if args.seq_limit:
         seq_limit(args.seq_limit)
         return

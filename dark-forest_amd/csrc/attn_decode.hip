@@ -244,30 +244,63 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
 
 // Merges the split-K partials of one head (attention_fused.cu:712-757):
 // m = max_c m_c, l = sum_c l_c exp(m_c - m), out = sum_c exp(m_c - m) o_c / l.
-// Chunks whose m_c is not above -FLT_MAX hold no key and are skipped.
-__global__ __launch_bounds__(64) void decode_reduce_kernel(const float *__restrict__ part_m,
-                                                           const float *__restrict__ part_l,
-                                                           const float *__restrict__ part_o,
-                                                           float *__restrict__ out, float *__restrict__ lse,
-                                                           int n_chunks, int D) {
-  const int h = blockIdx.x, lane = threadIdx.x;
+// Chunks whose m_c is not above -FLT_MAX hold no key and are skipped. 256
+// threads per head: the chunks are strided over the threads (and, for o,
+// over 4 groups of 64 columns), so the partial loads are independent of each
+// other instead of one chained loop.
+constexpr int kRedThreads = 256;
+__device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_max) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = is_max ? wave_max(v) : wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kRedThreads / 64; ++w) r = is_max ? fmaxf(r, scratch[w]) : r + scratch[w];
+  return r;
+}
+
+__global__ __launch_bounds__(kRedThreads) void decode_reduce_kernel(const float *__restrict__ part_m,
+                                                                    const float *__restrict__ part_l,
+                                                                    const float *__restrict__ part_o,
+                                                                    float *__restrict__ out, float *__restrict__ lse,
+                                                                    int n_chunks, int D) {
+  __shared__ float scratch[kRedThreads / 64];
+  __shared__ float acc_lds[kRedThreads / 64][128];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
   const float *pm = part_m + (size_t)h * n_chunks;
   const float *pl = part_l + (size_t)h * n_chunks;
+  const float *po = part_o + (size_t)h * n_chunks * D;
+  constexpr float kNoKey = -3.402823466e38f;  // -FLT_MAX, the reference's empty-chunk mark
   float mm = -INFINITY;
-  for (int cc = lane; cc < n_chunks; cc += 64) mm = fmaxf(mm, pm[cc]);
-  mm = wave_max(mm);
+  for (int cc = tid; cc < n_chunks; cc += kRedThreads) mm = fmaxf(mm, pm[cc]);
+  mm = block_reduce(mm, scratch, true);
   float ll = 0.f;
-  for (int cc = lane; cc < n_chunks; cc += 64)
-    if (pm[cc] > -3.402823466e38f) ll += pl[cc] * __expf(pm[cc] - mm);
-  ll = wave_sum(ll);
-  const float inv = ll > 0.f ? 1.f / ll : 0.f;
-  for (int d = lane; d < D; d += 64) {
-    float acc = 0.f;
-    for (int cc = 0; cc < n_chunks; ++cc)
-      if (pm[cc] > -3.402823466e38f) acc += __expf(pm[cc] - mm) * part_o[((size_t)h * n_chunks + cc) * D + d];
-    out[(size_t)h * D + d] = acc * inv;
+  for (int cc = tid; cc < n_chunks; cc += kRedThreads)
+    if (pm[cc] > kNoKey) ll += pl[cc] * __expf(pm[cc] - mm);
+  ll = block_reduce(ll, scratch, false);
+  // o: group grp takes chunks grp, grp+4, ...; lane d columns d and d+64.
+  float a0 = 0.f, a1 = 0.f;
+  for (int cc = grp; cc < n_chunks; cc += kRedThreads / 64) {
+    const float m_c = pm[cc];
+    const float w = m_c > kNoKey ? __expf(m_c - mm) : 0.f;
+    if (lane < D) a0 += w * po[(size_t)cc * D + lane];
+    if (lane + 64 < D) a1 += w * po[(size_t)cc * D + lane + 64];
   }
-  if (lane == 0 && lse) lse[h] = ll > 0.f ? mm + __logf(ll) : -INFINITY;
+  acc_lds[grp][lane] = a0;
+  acc_lds[grp][lane + 64] = a1;
+  __syncthreads();
+  if (grp == 0) {
+    const float inv = ll > 0.f ? 1.f / ll : 0.f;
+    for (int d = lane; d < D; d += 64) {
+      float o = 0.f;
+#pragma unroll
+      for (int g = 0; g < kRedThreads / 64; ++g) o += acc_lds[g][d];
+      out[(size_t)h * D + d] = o * inv;
+    }
+    if (lane == 0 && lse) lse[h] = ll > 0.f ? mm + __logf(ll) : -INFINITY;
+  }
 }
 
 }  // namespace
@@ -312,7 +345,7 @@ hipError_t launch_decode(const float *q, const void *k, const void *v, const int
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || a.n_chunks == 1) return err;
-  hipLaunchKernelGGL(decode_reduce_kernel, dim3((unsigned)n_heads), dim3(64), 0, stream, part_m, part_l,
+  hipLaunchKernelGGL(decode_reduce_kernel, dim3((unsigned)n_heads), dim3(kRedThreads), 0, stream, part_m, part_l,
                      part_o, out, lse, a.n_chunks, d_head);
   return hipGetLastError();
 }
