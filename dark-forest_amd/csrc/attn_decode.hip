@@ -244,11 +244,11 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeArgs a) {
 
 // Merges the split-K partials of one head (attention_fused.cu:712-757):
 // m = max_c m_c, l = sum_c l_c exp(m_c - m), out = sum_c exp(m_c - m) o_c / l.
-// Chunks whose m_c is not above -FLT_MAX hold no key and are skipped. 256
+// Chunks whose m_c is not above -FLT_MAX hold no key and are skipped. 512
 // threads per head: the chunks are strided over the threads (and, for o,
-// over 4 groups of 64 columns), so the partial loads are independent of each
+// over 8 groups of 64 columns), so the partial loads are independent of each
 // other instead of one chained loop.
-constexpr int kRedThreads = 256;
+constexpr int kRedThreads = 512;
 __device__ __forceinline__ float block_reduce(float v, float *scratch, bool is_max) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v = is_max ? wave_max(v) : wave_sum(v);
@@ -267,24 +267,48 @@ __global__ __launch_bounds__(kRedThreads) void decode_reduce_kernel(const float 
                                                                     float *__restrict__ out, float *__restrict__ lse,
                                                                     int n_chunks, int D) {
   __shared__ float scratch[kRedThreads / 64];
+  __shared__ float w_lds[kRedThreads];
   __shared__ float acc_lds[kRedThreads / 64][128];
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
+  constexpr int kGroups = kRedThreads / 64;
+  constexpr int kPre = 8;  // o values a lane loads before the weights are known
   const float *pm = part_m + (size_t)h * n_chunks;
   const float *pl = part_l + (size_t)h * n_chunks;
   const float *po = part_o + (size_t)h * n_chunks * D;
   constexpr float kNoKey = -3.402823466e38f;  // -FLT_MAX, the reference's empty-chunk mark
-  float mm = -INFINITY;
-  for (int cc = tid; cc < n_chunks; cc += kRedThreads) mm = fmaxf(mm, pm[cc]);
+  // Every load of the first kRedThreads chunks is issued at once: thread c
+  // takes chunk c's (m, l); lane d of group g takes o[c][d] of chunks
+  // c = g + 8i, i < kPre.
+  const bool mine = tid < n_chunks;
+  const float m_c = mine ? pm[tid] : -INFINITY, l_c = mine ? pl[tid] : 0.f;
+  float o0[kPre], o1[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int cc = grp + kGroups * i;
+    o0[i] = cc < n_chunks && lane < D ? po[(size_t)cc * D + lane] : 0.f;
+    o1[i] = cc < n_chunks && lane + 64 < D ? po[(size_t)cc * D + lane + 64] : 0.f;
+  }
+  float mm = m_c;
+  for (int cc = tid + kRedThreads; cc < n_chunks; cc += kRedThreads) mm = fmaxf(mm, pm[cc]);
   mm = block_reduce(mm, scratch, true);
-  float ll = 0.f;
-  for (int cc = tid; cc < n_chunks; cc += kRedThreads)
+  const float w_c = m_c > kNoKey ? __expf(m_c - mm) : 0.f;
+  w_lds[tid] = w_c;
+  float ll = w_c * l_c;
+  for (int cc = tid + kRedThreads; cc < n_chunks; cc += kRedThreads)
     if (pm[cc] > kNoKey) ll += pl[cc] * __expf(pm[cc] - mm);
-  ll = block_reduce(ll, scratch, false);
-  // o: group grp takes chunks grp, grp+4, ...; lane d columns d and d+64.
+  ll = block_reduce(ll, scratch, false);  // (its barriers also publish w_lds)
   float a0 = 0.f, a1 = 0.f;
-  for (int cc = grp; cc < n_chunks; cc += kRedThreads / 64) {
-    const float m_c = pm[cc];
-    const float w = m_c > kNoKey ? __expf(m_c - mm) : 0.f;
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int cc = grp + kGroups * i;
+    if (cc < kRedThreads) {
+      a0 += w_lds[cc] * o0[i];
+      a1 += w_lds[cc] * o1[i];
+    }
+  }
+  for (int cc = grp + kGroups * kPre; cc < n_chunks; cc += kGroups) {
+    const float m2 = pm[cc];
+    const float w = cc < kRedThreads ? w_lds[cc] : (m2 > kNoKey ? __expf(m2 - mm) : 0.f);
     if (lane < D) a0 += w * po[(size_t)cc * D + lane];
     if (lane + 64 < D) a1 += w * po[(size_t)cc * D + lane + 64];
   }
@@ -296,7 +320,7 @@ __global__ __launch_bounds__(kRedThreads) void decode_reduce_kernel(const float 
     for (int d = lane; d < D; d += 64) {
       float o = 0.f;
 #pragma unroll
-      for (int g = 0; g < kRedThreads / 64; ++g) o += acc_lds[g][d];
+      for (int g = 0; g < kGroups; ++g) o += acc_lds[g][d];
       out[(size_t)h * D + d] = o * inv;
     }
     if (lane == 0 && lse) lse[h] = ll > 0.f ? mm + __logf(ll) : -INFINITY;
