@@ -198,6 +198,49 @@ int legacy_decode(const char *fn, const float *q, const void *k, const void *v, 
   return record_hip(err, fn);
 }
 
+// ---- the elementwise companions (attention_fused.cu:1123-1231) -------------
+
+int pos_embed_impl(const float *table, float *out, uint32_t pos, uint32_t trained, uint32_t max_ctx,
+                   uint32_t d_model) {
+  const char *fn = "launch_pos_embed_interpolate";
+  if (table == nullptr || out == nullptr)
+    return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  if (!aligned(table, 4) || !aligned(out, 4))
+    return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": misaligned pointer");
+  // The reference reads row trained - 1 = 2^32 - 1 of the table then.
+  if (trained == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": trained_ctx_len must be >= 1");
+  if (d_model == 0) return DFATTN_OK;
+  return record_hip(dfattn::launch_pos_embed_interpolate(table, out, pos, trained, max_ctx, d_model, nullptr), fn);
+}
+
+int rope_impl(float *qk, uint32_t pos, uint32_t n_heads, uint32_t d_head, float base) {
+  const char *fn = "launch_apply_rope";
+  if (qk == nullptr) return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  if (!aligned(qk, 4)) return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": misaligned pointer");
+  // The reference's launch (grid n_heads, block d_head / 2) is invalid for these.
+  if (n_heads == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": n_heads must be >= 1");
+  if (d_head < 2) return record_error(DFATTN_ERR_HEAD_DIM, std::string(fn) + ": d_head must be >= 2");
+  if ((uint64_t)n_heads * d_head > (1ull << 32))
+    return record_error(DFATTN_ERR_OVERFLOW, std::string(fn) + ": n_heads * d_head is too large");
+  return record_hip(dfattn::launch_apply_rope(qk, pos, n_heads, d_head, base, nullptr), fn);
+}
+
+int paged_copy_impl(const char *fn, const float *src, void *pool, bool bf16, int32_t phys_block,
+                    uint32_t page_offset, uint32_t page_size, uint32_t d_model) {
+  if (src == nullptr || pool == nullptr)
+    return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  if (!aligned(src, 4) || !aligned(pool, bf16 ? 2 : 4))
+    return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": misaligned pointer");
+  // The reference's caller (paged_kv.rs:206-209) always passes a block from
+  // the pool's allocator and page_offset = pos % page_size.
+  if (phys_block < 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": phys_block must be >= 0");
+  if (page_offset >= page_size)
+    return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": page_offset must be < page_size");
+  if (d_model == 0) return DFATTN_OK;
+  return record_hip(
+      dfattn::launch_paged_copy_row(src, pool, bf16, phys_block, page_offset, page_size, d_model, nullptr), fn);
+}
+
 }  // namespace
 
 extern "C" {
@@ -412,6 +455,27 @@ void launch_paged_mha_decode_kv_bf16(const float *q, const uint16_t *k_pool, con
   mark_pending_if_failed(legacy_decode("launch_paged_mha_decode_kv_bf16", q, k_pool, v_pool, block_table,
                                        true, page_size, true, nullptr, nullptr, nullptr, out, n_heads,
                                        cur_seq_len, d_head, scale, 0, false));
+}
+
+void launch_pos_embed_interpolate(const float *pos_table, float *out, uint32_t pos, uint32_t trained_ctx_len,
+                                  uint32_t max_ctx_len, uint32_t d_model) {
+  mark_pending_if_failed(pos_embed_impl(pos_table, out, pos, trained_ctx_len, max_ctx_len, d_model));
+}
+
+void launch_apply_rope(float *qk, uint32_t pos, uint32_t n_heads, uint32_t d_head, float base_freq) {
+  mark_pending_if_failed(rope_impl(qk, pos, n_heads, d_head, base_freq));
+}
+
+void launch_paged_copy_row(const float *src, float *pool, int32_t phys_block, uint32_t page_offset,
+                           uint32_t page_size, uint32_t d_model) {
+  mark_pending_if_failed(
+      paged_copy_impl("launch_paged_copy_row", src, pool, false, phys_block, page_offset, page_size, d_model));
+}
+
+void launch_paged_copy_row_f32_to_bf16(const float *src, uint16_t *pool, int32_t phys_block, uint32_t page_offset,
+                                       uint32_t page_size, uint32_t d_model) {
+  mark_pending_if_failed(paged_copy_impl("launch_paged_copy_row_f32_to_bf16", src, pool, true, phys_block,
+                                         page_offset, page_size, d_model));
 }
 
 size_t dfattn_decode_workspace_bytes(uint32_t n_heads, uint32_t cur_seq_len, uint32_t d_head) {

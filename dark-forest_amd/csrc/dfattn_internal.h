@@ -297,4 +297,15 @@ hipError_t launch_decode(const float *q, const void *k, const void *v, const int
                          int d_head, float scale, int chunk, float *part_m, float *part_l, float *part_o,
                          bool fast, hipStream_t stream);
 
+// Elementwise companions of the decode path (attn_aux.hip). trained >= 1.
+hipError_t launch_pos_embed_interpolate(const float *table, float *out, unsigned pos, unsigned trained,
+                                        unsigned max_ctx, unsigned d_model, hipStream_t stream);
+// In place on qk [n_heads * d_head]; an odd d_head leaves its last value alone.
+hipError_t launch_apply_rope(float *qk, unsigned pos, unsigned n_heads, unsigned d_head, float base,
+                             hipStream_t stream);
+// pool row (phys_block * page_size + page_offset) := src [d_model], as fp32 or
+// as bf16 bit patterns rounded to nearest even.
+hipError_t launch_paged_copy_row(const float *src, void *pool, bool bf16, int phys_block, unsigned page_offset,
+                                 unsigned page_size, unsigned d_model, hipStream_t stream);
+
 }  // namespace dfattn

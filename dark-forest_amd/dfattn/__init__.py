@@ -57,6 +57,10 @@ SYMBOLS = {
     "launch_paged_mha_decode_kv": (None, [_P] * 5 + [_U32, _U32, _U32, _F, _U32]),
     "launch_paged_mha_decode_kv_splitk": (None, [_P] * 8 + [_U32, _U32, _U32, _F, _U32, _U32]),
     "launch_paged_mha_decode_kv_bf16": (None, [_P] * 5 + [_U32, _U32, _U32, _F, _U32]),
+    "launch_pos_embed_interpolate": (None, [_P, _P, _U32, _U32, _U32, _U32]),
+    "launch_apply_rope": (None, [_P, _U32, _U32, _U32, _F]),
+    "launch_paged_copy_row": (None, [_P, _P, ctypes.c_int32, _U32, _U32, _U32]),
+    "launch_paged_copy_row_f32_to_bf16": (None, [_P, _P, ctypes.c_int32, _U32, _U32, _U32]),
     "dfattn_decode_workspace_bytes": (ctypes.c_size_t, [_U32, _U32, _U32]),
     "dfattn_decode": (ctypes.c_int, [_P] * 4 + [_U32, _U32, _P, _P, _U32, _U32, _U32, _F, _P, ctypes.c_size_t, _P]),
     "dfattn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -339,6 +343,30 @@ def launch_paged_mha_decode_kv_bf16(q, k_pool, v_pool, block_table, out, n_heads
     """attention_fused.cu:1075 (bf16 pools as bit patterns), null stream."""
     lib().launch_paged_mha_decode_kv_bf16(_dev_ptr(q), _dev_any(k_pool), _dev_any(v_pool), _dev_any(block_table),
                                           _dev_ptr(out), n_heads, cur_seq_len, d_head, scale, page_size)
+
+
+# ---------------------------------------------------------------- elementwise companions (attention_fused.cu:1098-1231)
+def launch_pos_embed_interpolate(pos_table, out, pos, trained_ctx_len, max_ctx_len, d_model):
+    """attention_fused.cu:1123, null stream: out [d_model] := row pos of pos_table, or its linear
+    interpolation at pos * (trained - 1) / (max - 1) outside the trained range."""
+    lib().launch_pos_embed_interpolate(_dev_ptr(pos_table), _dev_ptr(out), pos, trained_ctx_len, max_ctx_len, d_model)
+
+
+def launch_apply_rope(qk, pos, n_heads, d_head, base_freq):
+    """attention_fused.cu:1164, null stream: rotary embedding of qk [n_heads * d_head] in place."""
+    lib().launch_apply_rope(_dev_ptr(qk), pos, n_heads, d_head, base_freq)
+
+
+def launch_paged_copy_row(src, pool, phys_block, page_offset, page_size, d_model):
+    """attention_fused.cu:1192, null stream: pool row phys_block * page_size + page_offset := src."""
+    lib().launch_paged_copy_row(_dev_ptr(src), _dev_ptr(pool), phys_block, page_offset, page_size, d_model)
+
+
+def launch_paged_copy_row_f32_to_bf16(src, pool, phys_block, page_offset, page_size, d_model):
+    """attention_fused.cu:1219, null stream: the same into a bf16 pool (int16 / uint16 / bfloat16 bits),
+    rounded to nearest even."""
+    lib().launch_paged_copy_row_f32_to_bf16(_dev_ptr(src), _dev_any(pool), phys_block, page_offset, page_size,
+                                            d_model)
 
 
 

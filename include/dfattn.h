@@ -145,6 +145,36 @@ void launch_paged_mha_decode_kv_bf16(const float *q, const uint16_t *k_pool,
                                      uint32_t d_head, float scale,
                                      uint32_t page_size);
 
+/* The elementwise kernels that share the reference's attention object. All
+ * run on the null stream; argument errors are recorded for darkforest_sync. */
+
+/* attention_fused.cu:1123 — out [d_model] := row pos of the trained table
+ * [trained_ctx_len, d_model] when pos < trained_ctx_len and max_ctx_len <=
+ * trained_ctx_len; otherwise the linear interpolation at position
+ * pos * (trained_ctx_len - 1) / (max_ctx_len - 1). A position past the
+ * table's last row (where the reference reads out of bounds) gives the last
+ * row. trained_ctx_len 0 is an argument error.                             */
+void launch_pos_embed_interpolate(const float *pos_table, float *out,
+                                  uint32_t pos, uint32_t trained_ctx_len,
+                                  uint32_t max_ctx_len, uint32_t d_model);
+/* attention_fused.cu:1164 — rotary embedding of one row qk [n_heads *
+ * d_head] in place: values (2i, 2i+1) of each head rotated by the angle
+ * pos * base_freq^(-2i / d_head). n_heads 0 and d_head < 2 (an invalid
+ * launch in the reference) are argument errors.                            */
+void launch_apply_rope(float *qk, uint32_t pos, uint32_t n_heads,
+                       uint32_t d_head, float base_freq);
+/* attention_fused.cu:1192 — row phys_block * page_size + page_offset of a
+ * paged pool [n_blocks * page_size, d_model] := src [d_model]. A negative
+ * phys_block or page_offset >= page_size is an argument error.            */
+void launch_paged_copy_row(const float *src, float *pool, int32_t phys_block,
+                           uint32_t page_offset, uint32_t page_size,
+                           uint32_t d_model);
+/* attention_fused.cu:1219 — the same into a bf16 pool (bit patterns as
+ * uint16), each value rounded to nearest even.                             */
+void launch_paged_copy_row_f32_to_bf16(const float *src, uint16_t *pool,
+                                       int32_t phys_block, uint32_t page_offset,
+                                       uint32_t page_size, uint32_t d_model);
+
 /* matmul.cu:21 — device synchronize; on a HIP error, or on an argument
  * error of one of the launchers above since the last sync, print
  * "[darkforest] ..." to stderr and abort(), as the reference does. Errors

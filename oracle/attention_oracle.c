@@ -27,6 +27,14 @@
  *   oracle_decode_f32           attention_fused.cu:551-615, 800-866, 968-1033
  *                               (single-query KV-cache decode: contiguous,
  *                               paged, bf16 pools), plus its logsumexp.
+ *   oracle_pos_embed_interpolate_f32
+ *                               attention_fused.cu:1098-1121 (position
+ *                               interpolation of a trained embedding table).
+ *   oracle_apply_rope_f32/_f64  attention_fused.cu:1139-1162 (rotary
+ *                               embedding of one row, in place).
+ *   oracle_paged_copy_row, oracle_f32_to_bf16
+ *                               attention_fused.cu:1178-1217 (a row written
+ *                               into a paged fp32 or bf16 pool).
  *
  * Arithmetic follows the reference: fp32 throughout, sums accumulated
  * sequentially in index order, exp from libm (Rust's f32::exp), mul and add
@@ -47,7 +55,13 @@
  *     sum_i dO_i; constant V gives constant O;
  *   - an independent vectorised float64 numpy implementation on seeded inputs;
  *   - planted mistakes (oracle_set_mutation) that each of those checks must
- *     catch.
+ *     catch;
+ *   - for the elementwise kernels: a linear table (interpolation is exact on
+ *     it up to rounding) and the trained-range copy; RoPE as the complex
+ *     product z * exp(i pos theta) in float64, pos 0 = identity, preserved
+ *     pair norms; the bf16 rounding against torch's own float -> bfloat16
+ *     conversion, including ties, overflow, subnormals, infinities and NaN;
+ *     a row written by oracle_paged_copy_row is the row oracle_decode reads.
  */
 #include <math.h>
 #include <stddef.h>
@@ -70,7 +84,12 @@ enum {
   MUT_HEAD_INDEX = 6,        /* K read from head H-1-h                      */
   MUT_LSE_LOG2 = 7,          /* lse in log base 2                           */
   MUT_DV_FROM_DS = 8,        /* dV accumulates dS instead of P              */
-  MUT_TRANSPOSE_DQ = 9       /* dQ uses q where k belongs                   */
+  MUT_TRANSPOSE_DQ = 9,      /* dQ uses q where k belongs                   */
+  MUT_ROPE_SIN_SIGN = 10,    /* RoPE rotates by -angle                      */
+  MUT_ROPE_FREQ = 11,        /* RoPE theta = base^(-i / d_head)             */
+  MUT_INTERP_SAME_ROW = 12,  /* interpolation between row p0 and itself     */
+  MUT_BF16_TRUNCATE = 13,    /* bf16 by truncation instead of rounding      */
+  MUT_PAGE_OFFSET = 14       /* paged row written at offset page_offset - 1 */
 };
 static int g_mutation = MUT_NONE;
 
@@ -397,6 +416,87 @@ static inline float bf16_to_f32(uint16_t b) {
 
 DEFINE_DECODE(oracle_decode_f32, float, expf, logf, fmaf)
 DEFINE_DECODE(oracle_decode_f64, double, exp, log, fma)
+
+/* ------------------------------------------------------------------------
+ * The elementwise kernels beside the decode family, one row each, in the
+ * reference's fp32 arithmetic.
+ * ---------------------------------------------------------------------- */
+
+/* attention_fused.cu:1098-1121: copy inside the trained range, else linear
+ * interpolation at pos * (trained - 1) / (max_ctx - 1) between rows p0 =
+ * trunc and p1 = min(p0 + 1, trained - 1). New: where p0 would lie past the
+ * table (the reference reads out of bounds there) the last row is returned.
+ * trained >= 1. */
+void oracle_pos_embed_interpolate_f32(const float *table, float *out, uint32_t pos,
+                                      uint32_t trained, uint32_t max_ctx,
+                                      uint32_t d_model) {
+  for (uint32_t d = 0; d < d_model; ++d) {
+    if (pos < trained && max_ctx <= trained) {
+      out[d] = table[(size_t)pos * d_model + d];
+      continue;
+    }
+    const float scale = (float)(trained - 1) / (float)(max_ctx - 1);
+    const float p_scaled = (float)pos * scale;
+    uint32_t p0 = (uint32_t)p_scaled;
+    float alpha = p_scaled - (float)p0;
+    if (p0 >= trained) {
+      p0 = trained - 1;
+      alpha = 0.0f;
+    }
+    uint32_t p1 = p0 + 1 < trained ? p0 + 1 : trained - 1;
+    if (g_mutation == MUT_INTERP_SAME_ROW) p1 = p0; /* planted */
+    const float v0 = table[(size_t)p0 * d_model + d];
+    const float v1 = table[(size_t)p1 * d_model + d];
+    out[d] = (1.0f - alpha) * v0 + alpha * v1;
+  }
+}
+
+/* attention_fused.cu:1139-1162: values (2i, 2i+1) of every head of one row
+ * rotated in place by pos * base^(-2i / d_head); an odd d_head leaves the
+ * last value alone. */
+#define DEFINE_ROPE(NAME, T, POW, COS, SIN)                                      \
+  void NAME(T *qk, uint32_t pos, uint32_t n_heads, uint32_t d_head, T base) {    \
+    for (uint32_t h = 0; h < n_heads; ++h)                                       \
+      for (uint32_t i = 0; i < d_head / 2; ++i) {                                \
+        const T two = g_mutation == MUT_ROPE_FREQ ? (T)1 : (T)2; /* planted */   \
+        const T theta = POW(base, -two * (T)i / (T)d_head);                      \
+        const T angle = (T)pos * theta;                                          \
+        const T c = COS(angle);                                                  \
+        const T s = g_mutation == MUT_ROPE_SIN_SIGN ? -SIN(angle) : SIN(angle);  \
+        const size_t i0 = (size_t)h * d_head + 2 * (size_t)i;                    \
+        const T x0 = qk[i0], x1 = qk[i0 + 1];                                    \
+        qk[i0] = x0 * c - x1 * s;                                                \
+        qk[i0 + 1] = x0 * s + x1 * c;                                            \
+      }                                                                          \
+  }
+
+DEFINE_ROPE(oracle_apply_rope_f32, float, powf, cosf, sinf)
+DEFINE_ROPE(oracle_apply_rope_f64, double, pow, cos, sin)
+
+/* fp32 -> bf16 bit pattern, round to nearest even (__float2bfloat16_rn of
+ * attention_fused.cu:1212); a NaN stays a NaN of the same sign, made quiet. */
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  if (g_mutation == MUT_BF16_TRUNCATE) return (uint16_t)(u >> 16); /* planted */
+  const uint32_t lsb = (u >> 16) & 1u;
+  return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+
+/* attention_fused.cu:1178-1217: pool row phys_block * page_size + page_offset
+ * := src, as fp32 (pool_bf16 = 0) or as bf16 bit patterns. */
+void oracle_paged_copy_row(const float *src, void *pool, int pool_bf16, int32_t phys_block,
+                           uint32_t page_offset, uint32_t page_size, uint32_t d_model) {
+  const uint32_t off = g_mutation == MUT_PAGE_OFFSET && page_offset > 0 ? page_offset - 1 : page_offset;
+  const size_t row = ((size_t)phys_block * page_size + off) * d_model; /* planted above */
+  for (uint32_t d = 0; d < d_model; ++d) {
+    if (pool_bf16)
+      ((uint16_t *)pool)[row + d] = oracle_f32_to_bf16(src[d]);
+    else
+      ((float *)pool)[row + d] = src[d];
+  }
+}
 
 /* Number of threads OpenMP would use by default (1 without OpenMP). */
 int oracle_max_threads(void) {

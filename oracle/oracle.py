@@ -33,7 +33,14 @@ MUTATIONS = {
     "lse_log2": 7,
     "dv_from_ds": 8,
     "transpose_dq": 9,
+    "rope_sin_sign": 10,
+    "rope_freq": 11,
+    "interp_same_row": 12,
+    "bf16_truncate": 13,
+    "page_offset": 14,
 }
+# Mistakes planted in the elementwise restatements (RoPE, interpolation, paged copy, bf16).
+AUX_MUTATIONS = ("rope_sin_sign", "rope_freq", "interp_same_row", "bf16_truncate", "page_offset")
 
 
 def build() -> str:
@@ -63,6 +70,16 @@ def _load():
     lib.oracle_decode_f32.argtypes = [f32p, vp, vp, i32p, c_int, c_int, f32p, f32p, c_int, c_int, c_int, c_float]
     lib.oracle_decode_f64.argtypes = [f64p, vp, vp, i32p, c_int, c_int, f64p, f64p, c_int, c_int, c_int, c_double]
     lib.oracle_decode_f32.restype = lib.oracle_decode_f64.restype = None
+    u32 = ctypes.c_uint32
+    lib.oracle_pos_embed_interpolate_f32.argtypes = [f32p, f32p, u32, u32, u32, u32]
+    lib.oracle_apply_rope_f32.argtypes = [f32p, u32, u32, u32, c_float]
+    lib.oracle_apply_rope_f64.argtypes = [f64p, u32, u32, u32, c_double]
+    lib.oracle_paged_copy_row.argtypes = [f32p, vp, c_int, ctypes.c_int32, u32, u32, u32]
+    lib.oracle_f32_to_bf16.argtypes = [c_float]
+    lib.oracle_f32_to_bf16.restype = ctypes.c_uint16
+    for fn in (lib.oracle_pos_embed_interpolate_f32, lib.oracle_apply_rope_f32, lib.oracle_apply_rope_f64,
+               lib.oracle_paged_copy_row):
+        fn.restype = None
     lib.oracle_set_mutation.argtypes = [c_int]
     lib.oracle_get_mutation.restype = c_int
     lib.oracle_max_threads.restype = c_int
@@ -177,6 +194,46 @@ def decode(q, k_cache, v_cache, n_heads, cur_len, scale, block_table=None, page_
     if cur_len <= 0:
         return None, None
     return out, lse
+
+
+def pos_embed_interpolate(table, pos, trained_ctx_len, max_ctx_len):
+    """attention_fused.cu:1098-1121 on table [trained, d_model]; returns out [d_model]."""
+    lib = _load()
+    table = _as(table, np.float32)
+    d_model = table.shape[-1]
+    out = np.full(d_model, np.nan, dtype=np.float32)
+    lib.oracle_pos_embed_interpolate_f32(_ptr(table, ctypes.c_float), _ptr(out, ctypes.c_float), int(pos),
+                                         int(trained_ctx_len), int(max_ctx_len), d_model)
+    return out
+
+
+def apply_rope(qk, pos, n_heads, d_head, base_freq, dtype=np.float32):
+    """attention_fused.cu:1139-1162 on a copy of qk [n_heads * d_head]; returns the rotated row."""
+    lib = _load()
+    ct = ctypes.c_float if dtype == np.float32 else ctypes.c_double
+    x = _as(qk, dtype).reshape(-1).copy()
+    fn = lib.oracle_apply_rope_f32 if dtype == np.float32 else lib.oracle_apply_rope_f64
+    fn(_ptr(x, ct), int(pos), int(n_heads), int(d_head), ct(base_freq))
+    return x
+
+
+def paged_copy_row(src, pool, phys_block, page_offset, page_size):
+    """attention_fused.cu:1178-1217: writes src into row phys_block * page_size + page_offset of pool
+    (float32, or uint16 bf16 bit patterns) in place."""
+    lib = _load()
+    src = _as(src, np.float32).reshape(-1)
+    assert pool.flags["C_CONTIGUOUS"] and pool.dtype in (np.float32, np.uint16)
+    lib.oracle_paged_copy_row(_ptr(src, ctypes.c_float), pool.ctypes.data_as(ctypes.c_void_p),
+                              int(pool.dtype == np.uint16), int(phys_block), int(page_offset), int(page_size),
+                              src.size)
+    return pool
+
+
+def f32_to_bf16(a):
+    """fp32 -> bf16 bit patterns through the oracle's scalar rounding (NaN-aware), as uint16."""
+    lib = _load()
+    flat = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    return np.array([lib.oracle_f32_to_bf16(float(x)) for x in flat], dtype=np.uint16).reshape(np.shape(a))
 
 
 def to_bf16_bits(a):

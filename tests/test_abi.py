@@ -230,3 +230,33 @@ def test_legacy_decode_split_with_zero_chunk_is_recorded():
     lib.launch_paged_mha_decode_kv(FAKE, FAKE, FAKE, FAKE, FAKE, 12, 100, 64, 0.1, 0)
     assert lib.dfattn_last_error() == -3
     lib.dfattn_clear_error()
+
+
+@pytest.mark.parametrize("call,status", [
+    (lambda l: l.launch_pos_embed_interpolate(None, FAKE, 0, 10, 10, 64), -1),
+    (lambda l: l.launch_pos_embed_interpolate(FAKE, FAKE, 3, 0, 10, 64), -3),   # the reference reads row 2^32-1
+    (lambda l: l.launch_apply_rope(None, 1, 12, 64, 1e4), -1),
+    (lambda l: l.launch_apply_rope(FAKE, 1, 0, 64, 1e4), -3),                   # grid 0: invalid launch there
+    (lambda l: l.launch_apply_rope(FAKE, 1, 12, 1, 1e4), -4),                   # block 0: invalid launch there
+    (lambda l: l.launch_apply_rope(FAKE, 1, 65536, 65537, 1e4), -5),
+    (lambda l: l.launch_paged_copy_row(FAKE, None, 0, 0, 16, 768), -1),
+    (lambda l: l.launch_paged_copy_row(FAKE, FAKE, -1, 0, 16, 768), -3),
+    (lambda l: l.launch_paged_copy_row(FAKE, FAKE, 2, 16, 16, 768), -3),        # offset outside its page
+    (lambda l: l.launch_paged_copy_row_f32_to_bf16(FAKE, ctypes.c_void_p(0x10001), 0, 0, 16, 768), -2),
+    (lambda l: l.launch_paged_copy_row_f32_to_bf16(FAKE, FAKE, 0, 3, 2, 768), -3),
+])
+def test_elementwise_launchers_record_argument_errors(call, status):
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    call(lib)
+    assert lib.dfattn_last_error() == status
+    lib.dfattn_clear_error()
+
+
+def test_elementwise_launchers_with_nothing_to_do_launch_nothing():
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    lib.launch_pos_embed_interpolate(FAKE, FAKE, 3, 10, 10, 0)
+    lib.launch_paged_copy_row(FAKE, FAKE, 0, 0, 16, 0)
+    lib.launch_paged_copy_row_f32_to_bf16(FAKE, FAKE, 0, 0, 16, 0)
+    assert lib.dfattn_last_error() == 0
