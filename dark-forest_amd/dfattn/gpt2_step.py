@@ -27,6 +27,7 @@ comparator, scripts/verify_loss_parity.py:58) for loss-parity checks.
 from __future__ import annotations
 
 import math
+import struct
 import time
 
 from . import FusedCausalAttention
@@ -80,7 +81,11 @@ class StaticGPT2:
         self.ln_f_g = const(1, d_model)
         self.ln_f_b = const(0, d_model)
         self.lm_head = randn(vocab_size, d_model)
-        self.opt = torch.optim.AdamW(self.parameters(), lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        # The engine keeps its hyper-parameters as f32 (static_gpt2.rs:518-521), which its checkpoint
+        # footer stores; holding the same f32 values makes a resumed run continue bit for bit.
+        f32 = lambda x: struct.unpack("<f", struct.pack("<f", x))[0]  # noqa: E731
+        self.opt = torch.optim.AdamW(self.parameters(), lr=f32(lr), betas=(f32(0.9), f32(0.95)), eps=f32(1e-8),
+                                     weight_decay=f32(0.1))
         self.pos_idx = torch.arange(seq_len, device=self.device)
 
     def parameters(self):

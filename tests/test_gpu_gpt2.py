@@ -49,3 +49,35 @@ def test_full_gpt2_small_initial_loss_and_descent(device):
         last = float(model.step(tokens, targets))
     say(f"loss after 4 steps {last:.4f}")
     assert math.isfinite(last) and last < first
+
+
+def test_checkpoints_carry_the_gpu_model(device, tmp_path):
+    """The reference's binary checkpoint resumes the GPU run; its safetensors export loads the same
+    weights into a CPU PyTorch twin (SDPA attention), whose loss then matches within the parity bar."""
+    import torch
+
+    from dfattn import checkpoint as C
+
+    cfg = dict(vocab_size=500, d_model=128, n_heads=2, n_layers=2, d_ff=512, seq_len=256, lr=1e-3)
+    a = StaticGPT2(**cfg, seed=1, attention="dfattn")
+    tokens, targets = synthetic_batch(500, 256, 11, device)
+    for _ in range(2):
+        a.step(tokens, targets)
+    say("binary checkpoint: save, load into a fresh GPU model, one more step each")
+    C.save_checkpoint(a, tmp_path / "m.ckpt")
+    b = StaticGPT2(**cfg, seed=2, attention="dfattn")
+    C.load_checkpoint(b, tmp_path / "m.ckpt")
+    for wa, wb in zip(a.parameters(), b.parameters()):
+        assert torch.equal(wa, wb)
+    la, lb = float(a.step(tokens, targets)), float(b.step(tokens, targets))
+    say(f"resumed losses {la:.7f} {lb:.7f}")
+    assert abs(la - lb) <= 1e-6 * abs(la)
+    say("safetensors export into a CPU twin")
+    C.save_gpt2_safetensors(a, tmp_path / "m.safetensors")
+    twin = StaticGPT2(**cfg, seed=3, device="cpu", attention="sdpa")
+    C.load_gpt2_safetensors(twin, tmp_path / "m.safetensors")
+    with torch.no_grad():
+        ga = float(a.loss(tokens, targets))
+        gt = float(twin.loss(tokens.cpu(), targets.cpu()))
+    say(f"GPU {ga:.6f} CPU twin {gt:.6f}")
+    assert abs(ga - gt) < 1e-3
