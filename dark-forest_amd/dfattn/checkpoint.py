@@ -110,13 +110,15 @@ def load_checkpoint(model, path) -> None:
     with torch.no_grad():
         for w, v in zip(weights, values):
             w.copy_(torch.from_numpy(v.copy()).view_as(w))
+    g = _adam_group(model)
     for w, (m, v) in zip(weights, moments):
         model.opt.state[w] = {
-            "step": torch.tensor(float(steps), dtype=torch.float32),
+            # a fused or capturable AdamW keeps its step counts beside the parameters
+            "step": torch.tensor(float(steps), dtype=torch.float32,
+                                 device=w.device if g.get("capturable") or g.get("fused") else "cpu"),
             "exp_avg": torch.from_numpy(m.copy()).view_as(w).to(w.device),
             "exp_avg_sq": torch.from_numpy(v.copy()).view_as(w).to(w.device),
         }
-    g = _adam_group(model)
     g["lr"], g["betas"], g["eps"], g["weight_decay"] = lr, (b1, b2), eps, wd
 
 

@@ -43,7 +43,7 @@ class StaticGPT2:
     """GPT-2 with the reference engine's architecture, init and optimizer."""
 
     def __init__(self, vocab_size=50257, d_model=768, n_heads=12, n_layers=12, d_ff=3072, seq_len=1024, lr=3e-4,
-                 seed=0, device="cuda", attention="dfattn"):
+                 seed=0, device="cuda", attention="dfattn", capturable=False):
         torch = _torch()
         if d_model % n_heads:
             raise ValueError("d_model must be divisible by n_heads")
@@ -84,8 +84,14 @@ class StaticGPT2:
         # The engine keeps its hyper-parameters as f32 (static_gpt2.rs:518-521), which its checkpoint
         # footer stores; holding the same f32 values makes a resumed run continue bit for bit.
         f32 = lambda x: struct.unpack("<f", struct.pack("<f", x))[0]  # noqa: E731
+        # On the GPU the update is one fused kernel per parameter group (the engine's update is one
+        # kernel per tensor, lib.rs:1755-1788); the multi-pass foreach update costs about 2.8 ms more
+        # per GPT-2 small step. capturable: AdamW keeps its step counts on the device, so a step can
+        # be recorded into a graph.
         self.opt = torch.optim.AdamW(self.parameters(), lr=f32(lr), betas=(f32(0.9), f32(0.95)), eps=f32(1e-8),
-                                     weight_decay=f32(0.1))
+                                     weight_decay=f32(0.1), fused=self.device.type == "cuda",
+                                     capturable=capturable)
+        self._graph = None
         self.pos_idx = torch.arange(seq_len, device=self.device)
 
     def parameters(self):
@@ -133,6 +139,38 @@ class StaticGPT2:
         loss.backward()
         self.opt.step()
         return loss.detach()
+
+
+    def capture(self, tokens, targets, warmup=3):
+        """Record one whole training step into a HIP graph (the engine replays a captured step too,
+        static_gpt2.rs graph_exec) after `warmup` eager steps on a side stream, which allocate the
+        optimizer state and the autograd buffers. Returns the static loss tensor every replay() updates.
+        Needs capturable=True. The batch is copied into static buffers; set_batch() changes it."""
+        torch = _torch()
+        if not self.opt.param_groups[0]["capturable"]:
+            raise ValueError("StaticGPT2.capture needs capturable=True")
+        self._tokens, self._targets = tokens.clone(), targets.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.step(self._tokens, self._targets)
+        torch.cuda.current_stream().wait_stream(side)
+        self._graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._graph):
+            self._loss = self.step(self._tokens, self._targets)
+        return self._loss
+
+    def set_batch(self, tokens, targets):
+        self._tokens.copy_(tokens)
+        self._targets.copy_(targets)
+
+    def replay(self):
+        """One captured training step on the current batch; returns the static loss tensor."""
+        if self._graph is None:
+            raise RuntimeError("StaticGPT2.replay before capture")
+        self._graph.replay()
+        return self._loss
 
 
 def synthetic_batch(vocab_size, seq_len, seed, device):

@@ -81,3 +81,25 @@ def test_checkpoints_carry_the_gpu_model(device, tmp_path):
         gt = float(twin.loss(tokens.cpu(), targets.cpu()))
     say(f"GPU {ga:.6f} CPU twin {gt:.6f}")
     assert abs(ga - gt) < 1e-3
+
+
+def test_captured_step_replays_match_eager_steps(device):
+    """A step recorded into a HIP graph (capture, then replay with eager work and synchronisations between
+    the replays) gives the eager steps' losses and weights."""
+    import torch
+
+    cfg = dict(vocab_size=500, d_model=128, n_heads=2, n_layers=2, d_ff=512, seq_len=256, lr=1e-3, seed=4)
+    eager = StaticGPT2(**cfg, capturable=True)
+    graph = StaticGPT2(**cfg, capturable=True)
+    tokens, targets = synthetic_batch(500, 256, 13, device)
+    want = [float(eager.step(tokens, targets)) for _ in range(7)]
+    loss = graph.capture(tokens, targets, warmup=3)
+    for i in range(3, 7):
+        graph.replay()
+        torch.cuda.synchronize()
+        got = float(loss)
+        _ = torch.ones(4096, device=device).sum().item()
+        say(f"replay {i}: graph {got:.7f} eager {want[i]:.7f}")
+        assert abs(got - want[i]) <= 1e-6 * abs(want[i])
+    for a, b in zip(eager.parameters(), graph.parameters()):
+        assert torch.allclose(a, b, rtol=0, atol=1e-6)
