@@ -233,6 +233,49 @@ def summarize_trace(stats_csv):
     return "\n".join(lines)
 
 
+def _gpt2_kernel_class(name):
+    """Category of a kernel of the GPT-2 step (for the per-step breakdown)."""
+    low = name.lower()
+    for key, label in (("cijk", "GEMM (hipBLASLt fp32)"), ("fwd_d64", "attention forward (dfattn)"),
+                       ("bwd_main", "attention backward main (dfattn)"), ("bwd_pre", "attention backward phase 1 (dfattn)"),
+                       ("bwd_convert", "attention backward phase 1 (dfattn)"), ("fusedopti", "AdamW (fused)"),
+                       ("softmax", "softmax / cross-entropy"), ("nll", "softmax / cross-entropy"),
+                       ("layer_norm", "LayerNorm fwd/bwd"), ("gradgammabeta", "LayerNorm fwd/bwd"),
+                       ("reduce_kernel", "reductions (bias gradients, sums)"), ("fill", "fills")):
+        if key in low:
+            return label
+    return "elementwise (adds, GELU, embedding, ...)"
+
+
+def summarize_gpt2_trace(trace_csv, skip=3):
+    """Per-step GPU time of the GPT-2 steps in a rocprofv3 kernel_trace.csv of a bench.py run: the steps
+    begin at the first GEMM and each ends with its batch of fused-AdamW launches; the first `skip`
+    (the warmup) are left out."""
+    import collections
+    import csv
+
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    first = next(i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("Cijk"))
+    g = rows[first:]
+    opt = [i for i, r in enumerate(g) if "FusedOpti" in r["Kernel_Name"]]
+    ends = [a for a, b in zip(opt, opt[1:] + [None]) if b != a + 1]
+    starts = [0] + [e + 1 for e in ends[:-1]]
+    cat, busy, spans = collections.Counter(), 0.0, []
+    for s0, e in list(zip(starts, ends))[skip:]:
+        step = g[s0:e + 1]
+        spans.append((int(step[-1]["End_Timestamp"]) - int(step[0]["Start_Timestamp"])) / 1e6)
+        for r in step:
+            d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+            cat[_gpt2_kernel_class(r["Kernel_Name"])] += d
+            busy += d
+    n = len(spans)
+    lines = [f"{n} steps after {skip} warmup; GPU busy {busy / n:.3f} ms per step (kernel durations summed); "
+             f"first-to-last kernel span {sum(spans) / n:.3f} ms per step under the profiler",
+             "", "| kernels | ms per step | share |", "|---|---|---|"]
+    lines += [f"| {k} | {v / n:.3f} | {100 * v / busy:.1f}% |" for k, v in cat.most_common()]
+    return "\n".join(lines)
+
+
 SEQ_LIMIT_LENGTHS = (8192, 16384, 32768, 65536, 131072, 262144, 524288, 1048576, 2097152)
 
 
@@ -368,6 +411,8 @@ def main():
                     help="print the HBM-traffic summary of two rocprofv3 --pmc runs and exit (no GPU)")
     ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
                     help="print a rocprofv3 --kernel-trace --stats summary table and exit (no GPU)")
+    ap.add_argument("--summarize-gpt2-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-step kernel breakdown of the GPT-2 steps in a rocprofv3 kernel_trace.csv")
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
@@ -387,6 +432,9 @@ def main():
         return
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_gpt2_trace:
+        print(summarize_gpt2_trace(args.summarize_gpt2_trace))
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters))
