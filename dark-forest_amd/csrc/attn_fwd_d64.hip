@@ -419,12 +419,75 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     else
       __builtin_amdgcn_sched_barrier(0);  // keep the iterations' register live ranges apart
   };
+  // Register r of S^T holds key t*64 + 32*kh + 4*hh + 8*(r/4) + r%4; keys
+  // above the lane's row are masked.
+  auto mask_diag = [&](f32x16 &x, int tile) {
+    const int lim = key_lim - (tile * kBN + kh * 32 + hh * 4);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if ((r >> 2) * 8 + (r & 3) > lim) x[r] = -INFINITY;
+  };
+  // The two tiles on the causal diagonal (t and t+1, the last two) of a
+  // query tile that ends at or before S, as steady iterations with
+  // compile-time stages: tile t stores V of tile t+1 (the only staging left)
+  // and issues the scores of tile t+1; tile t+1 has no next tile. Waves that
+  // see no key of a tile compute fully masked scores (P = 0) instead of
+  // skipping it. The ring stages and barriers are those of `step`.
+  auto diag = [&](int t, auto stage) {
+    constexpr int p = decltype(stage)::value;
+    static_assert((p & 1) == 0, "the diagonal starts at an even tile");
+    half8_t kf[4], vf[2][2], pf[2];
+    read_k(p + 1, kf);
+    read_v(p + kStages - 1, vf);
+    f32x16 sn = scores(kf);
+    pv(vf, pprev);
+    mask_diag(s, t);
+    probs(s, pf);
+    float psum = rowsum(pf);
+    store_rows(vstage(p + 1), vreg[1]);
+    if (__any(psum >= kRescaleSum || m == -INFINITY))
+      softmax_fix(s, sn, pf, row_max(s), psum, std::false_type{});
+    else
+      l += psum;
+    s = sn;
+    pprev[0] = pf[0];
+    pprev[1] = pf[1];
+    __builtin_amdgcn_sched_barrier(0);
+    read_v(p, vf);
+    pv(vf, pprev);
+    mask_diag(s, t + 1);
+    probs(s, pf);
+    psum = rowsum(pf);
+    f32x16 none = f32x16{};  // no next tile
+    if (__any(psum >= kRescaleSum || m == -INFINITY))
+      softmax_fix(s, none, pf, row_max(s), psum, std::false_type{});
+    else
+      l += psum;
+    pprev[0] = pf[0];
+    pprev[1] = pf[1];
+    __syncthreads();
+  };
   int t = 0;
   for (; t + 4 <= n_main; t += 4) {
     iter(t, Stage<0>{});
     iter(t + 1, Stage<1>{});
     iter(t + 2, Stage<2>{});
     iter(t + 3, Stage<3>{});
+  }
+  // Under causal masking a query tile that ends at or before S has n_main =
+  // n_tiles - 2 (even): after the loop above at most two unmasked tiles
+  // remain (stages 0 and 1), then the diagonal pair.
+  if (causal && q_blk0 + kBM <= S) {
+    if (t + 2 <= n_main) {
+      iter(t, Stage<0>{});
+      iter(t + 1, Stage<1>{});
+      t += 2;
+    }
+    if ((t & 3) == 0)
+      diag(t, Stage<0>{});
+    else
+      diag(t, Stage<2>{});
+    t = n_tiles;
   }
   for (; t < n_tiles; ++t) step(t);
   // The last tile's product.
