@@ -237,6 +237,12 @@ def _gpt2_kernel_class(name):
     """Category of a kernel of the GPT-2 step (for the per-step breakdown)."""
     low = name.lower()
     for key, label in (("cijk", "GEMM (hipBLASLt fp32)"), ("fwd_d64", "attention forward (dfattn)"),
+                       ("ln_fwd", "LayerNorm fwd/bwd (dfgpt2)"), ("ln_bwd", "LayerNorm fwd/bwd (dfgpt2)"),
+                       ("colsum_vec_kernel<true", "LayerNorm fwd/bwd (dfgpt2)"),
+                       ("colsum_generic_kernel<true", "LayerNorm fwd/bwd (dfgpt2)"),
+                       ("colsum", "bias gradients (dfgpt2)"), ("gelu_kernel", "GELU fwd/bwd (dfgpt2)"),
+                       ("adamw_kernel", "AdamW (dfgpt2, one launch over the arena)"),
+                       ("step_advance", "AdamW (dfgpt2, one launch over the arena)"),
                        ("bwd_main", "attention backward main (dfattn)"), ("bwd_pre", "attention backward phase 1 (dfattn)"),
                        ("bwd_convert", "attention backward phase 1 (dfattn)"), ("fusedopti", "AdamW (fused)"),
                        ("softmax", "softmax / cross-entropy"), ("nll", "softmax / cross-entropy"),
@@ -249,15 +255,16 @@ def _gpt2_kernel_class(name):
 
 def summarize_gpt2_trace(trace_csv, skip=3):
     """Per-step GPU time of the GPT-2 steps in a rocprofv3 kernel_trace.csv of a bench.py run: the steps
-    begin at the first GEMM and each ends with its batch of fused-AdamW launches; the first `skip`
-    (the warmup) are left out."""
+    begin at the first GEMM and each ends with its optimizer launches (dfgpt2's AdamW, whose last
+    kernel advances the step count, or torch's fused AdamW); the first `skip` (the warmup) are left
+    out."""
     import collections
     import csv
 
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
     first = next(i for i, r in enumerate(rows) if r["Kernel_Name"].startswith("Cijk"))
     g = rows[first:]
-    opt = [i for i, r in enumerate(g) if "FusedOpti" in r["Kernel_Name"]]
+    opt = [i for i, r in enumerate(g) if "FusedOpti" in r["Kernel_Name"] or "step_advance" in r["Kernel_Name"]]
     ends = [a for a, b in zip(opt, opt[1:] + [None]) if b != a + 1]
     starts = [0] + [e + 1 for e in ends[:-1]]
     cat, busy, spans = collections.Counter(), 0.0, []
@@ -557,16 +564,23 @@ def main():
 
         log(f"GPT-2 small step (S=1024), {args.gpt2_steps} timed steps")
         model = StaticGPT2(seq_len=1024, seed=0)
-        g2 = time_steps(model, steps=args.gpt2_steps, warmup=3)
+        eager = time_steps(model, steps=args.gpt2_steps, warmup=3)
+        log(f"GPT-2 step median {eager['median_ms']:.2f} ms eager; now recorded into a HIP graph")
+        g2 = time_steps(model, steps=args.gpt2_steps, warmup=3, graph=True)
         result["gpt2_step_ms"] = round(g2["median_ms"], 3)
         result["gpt2_step"] = {"config": "12 layers, d_model 768, 12 heads, d_ff 3072, vocab 50257, S=1024, batch 1",
                                "weights": "fp32, N(0,0.02) seeded", "tokens": "uniform [0,50257) seeded",
+                               "timing": "replays of one step recorded into a HIP graph (StaticGPT2.capture), "
+                                         "each followed by a device sync; eager_* = the same step dispatched "
+                                         "from Python each time",
                                "median_ms": round(g2["median_ms"], 3), "min_ms": round(g2["min_ms"], 3),
+                               "eager_median_ms": round(eager["median_ms"], 3),
+                               "eager_min_ms": round(eager["min_ms"], 3),
                                "steps": args.gpt2_steps, "warmup": 3,
-                               "loss_first": round(g2["losses"][0], 4), "loss_last": round(g2["losses"][-1], 4),
+                               "loss_first": round(eager["losses"][0], 4), "loss_last": round(g2["losses"][-1], 4),
                                "peak_mem_mb": round(g2["peak_mem_mb"], 1)}
         del model
-        log(f"GPT-2 step median {g2['median_ms']:.2f} ms")
+        log(f"GPT-2 step median {g2['median_ms']:.2f} ms (graph replay)")
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.randn(n, device=dev)

@@ -41,6 +41,8 @@ int dfattn::record_error(int status, const std::string &msg) {
   return status;
 }
 
+void dfattn::mark_pending(int status) { mark_pending_if_failed(status); }
+
 namespace {
 using dfattn::record_error;
 

@@ -10,4 +10,8 @@ namespace dfattn {
 // dfattn_last_error_message) and returns status.
 int record_error(int status, const std::string &msg);
 
+// For the reference launcher symbols (void return): keeps a failed status
+// for darkforest_sync, which aborts on it.
+void mark_pending(int status);
+
 }  // namespace dfattn

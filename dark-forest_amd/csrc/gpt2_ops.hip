@@ -1,0 +1,563 @@
+// gpt2_ops.hip — the GPT-2 training step's non-attention kernels on gfx950:
+// LayerNorm forward and backward, tanh GELU forward and backward, the bias
+// gradient of a linear layer and the AdamW update.
+//
+// They replace the reference engine's launchers of the same names
+// (darkforest-cuda/kernels/layernorm.cu:97, 187; elementwise.cu:195, 217;
+// matmul.cu:240, 341), which the engine's step calls around its attention
+// (darkforest-core/src/engine/static_gpt2.rs:1315-1364, 1427-1543, 1661).
+// All of them are memory-bound (a few bytes per flop): rows are read as
+// float4 by wave64 lanes, LayerNorm keeps a row in registers (one wave per
+// row), and the column reductions (bias and LayerNorm parameter gradients)
+// give each workgroup 64 columns and a fixed summation order instead of the
+// reference's floating-point atomics, so every result is reproducible bit
+// for bit (AdamW's sign-sensitive update of a near-zero gradient depends on
+// that).
+#include "dfattn_internal.h"
+#include "dfattn_status.h"
+#include "dfgpt2.h"
+
+#include <climits>
+#include <initializer_list>
+#include <string>
+
+namespace dfattn {
+namespace {
+
+constexpr float kLnEps = 1e-5f;  // layernorm.cu:14
+// tanh GELU constants: sqrt(2/pi) and the cubic coefficient (elementwise.cu:181-182).
+constexpr float kGeluK0 = 0.7978845608028654f;
+constexpr float kGeluK1 = 0.044715f;
+
+__device__ __forceinline__ float4 splat4(float a) { return make_float4(a, a, a, a); }
+__device__ __forceinline__ float hsum4(float4 v) { return (v.x + v.y) + (v.z + v.w); }
+
+// ------------------------------------------------------------ LayerNorm forward
+// One wave per row, V float4 per lane held in registers (features <= 256 V,
+// features % 4 == 0, 16-byte aligned rows); four rows per 256-thread
+// workgroup. The mean, then the variance about it, as layernorm.cu:41-75.
+template <int V>
+__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta, float *__restrict__ out,
+                                                         float *__restrict__ means, float *__restrict__ rstds,
+                                                         int batch, int features) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= batch) return;
+  const int nv = features >> 2;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * features);
+  float4 v[V];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = c < nv ? xr[c] : splat4(0.f);
+    s += hsum4(v[i]);
+  }
+  const float mean = wave_sum(s) / (float)features;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (lane + 64 * i < nv) {
+      const float4 d = make_float4(v[i].x - mean, v[i].y - mean, v[i].z - mean, v[i].w - mean);
+      q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+    }
+  }
+  const float rstd = 1.f / sqrtf(wave_sum(q) / (float)features + kLnEps);
+  if (lane == 0) {
+    if (means) means[row] = mean;
+    if (rstds) rstds[row] = rstd;
+  }
+  float4 *orow = reinterpret_cast<float4 *>(out + (size_t)row * features);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nv) {
+      const float4 g = gamma ? reinterpret_cast<const float4 *>(gamma)[c] : splat4(1.f);
+      const float4 b = beta ? reinterpret_cast<const float4 *>(beta)[c] : splat4(0.f);
+      orow[c] = make_float4((v[i].x - mean) * rstd * g.x + b.x, (v[i].y - mean) * rstd * g.y + b.y,
+                            (v[i].z - mean) * rstd * g.z + b.z, (v[i].w - mean) * rstd * g.w + b.w);
+    }
+  }
+}
+
+// Any width and 4-byte alignment: one wave per row, three passes over the
+// row (it stays in the caches between them).
+__global__ __launch_bounds__(256) void ln_fwd_generic_kernel(const float *__restrict__ x,
+                                                             const float *__restrict__ gamma,
+                                                             const float *__restrict__ beta, float *__restrict__ out,
+                                                             float *__restrict__ means, float *__restrict__ rstds,
+                                                             int batch, int features) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= batch) return;
+  const float *xr = x + (size_t)row * features;
+  float s = 0.f;
+  for (int c = lane; c < features; c += 64) s += xr[c];
+  const float mean = wave_sum(s) / (float)features;
+  float q = 0.f;
+  for (int c = lane; c < features; c += 64) {
+    const float d = xr[c] - mean;
+    q += d * d;
+  }
+  const float rstd = 1.f / sqrtf(wave_sum(q) / (float)features + kLnEps);
+  if (lane == 0) {
+    if (means) means[row] = mean;
+    if (rstds) rstds[row] = rstd;
+  }
+  float *orow = out + (size_t)row * features;
+  for (int c = lane; c < features; c += 64)
+    orow[c] = (xr[c] - mean) * rstd * (gamma ? gamma[c] : 1.f) + (beta ? beta[c] : 0.f);
+}
+
+// ------------------------------------------------------ LayerNorm backward, dx
+// grad_x = rstd / F * (F ds - sum(ds) - x_hat sum(ds x_hat)), ds = grad_out *
+// gamma (layernorm.cu:126-178). One wave per row, row in registers.
+template <int V>
+__global__ __launch_bounds__(256) void ln_bwd_dx_vec_kernel(const float *__restrict__ dout, const float *__restrict__ x,
+                                                            const float *__restrict__ gamma,
+                                                            const float *__restrict__ means,
+                                                            const float *__restrict__ rstds, float *__restrict__ grad_x,
+                                                            int batch, int features) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= batch) return;
+  const int nv = features >> 2;
+  const float mean = means[row], rstd = rstds[row];
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * features);
+  const float4 *dr = reinterpret_cast<const float4 *>(dout + (size_t)row * features);
+  float4 xh[V], ds[V];
+  float sds = 0.f, sdsx = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    xh[i] = ds[i] = splat4(0.f);
+    if (c < nv) {
+      const float4 xv = xr[c], dv = dr[c];
+      const float4 g = gamma ? reinterpret_cast<const float4 *>(gamma)[c] : splat4(1.f);
+      xh[i] = make_float4((xv.x - mean) * rstd, (xv.y - mean) * rstd, (xv.z - mean) * rstd, (xv.w - mean) * rstd);
+      ds[i] = make_float4(dv.x * g.x, dv.y * g.y, dv.z * g.z, dv.w * g.w);
+      sds += hsum4(ds[i]);
+      sdsx += (ds[i].x * xh[i].x + ds[i].y * xh[i].y) + (ds[i].z * xh[i].z + ds[i].w * xh[i].w);
+    }
+  }
+  const float sum_ds = wave_sum(sds), sum_dsx = wave_sum(sdsx);
+  const float f = (float)features, k = rstd / f;
+  float4 *gr = reinterpret_cast<float4 *>(grad_x + (size_t)row * features);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nv)
+      gr[c] = make_float4(k * (f * ds[i].x - sum_ds - xh[i].x * sum_dsx), k * (f * ds[i].y - sum_ds - xh[i].y * sum_dsx),
+                          k * (f * ds[i].z - sum_ds - xh[i].z * sum_dsx), k * (f * ds[i].w - sum_ds - xh[i].w * sum_dsx));
+  }
+}
+
+__global__ __launch_bounds__(256) void ln_bwd_dx_generic_kernel(const float *__restrict__ dout,
+                                                                const float *__restrict__ x,
+                                                                const float *__restrict__ gamma,
+                                                                const float *__restrict__ means,
+                                                                const float *__restrict__ rstds,
+                                                                float *__restrict__ grad_x, int batch, int features) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= batch) return;
+  const float mean = means[row], rstd = rstds[row];
+  const float *xr = x + (size_t)row * features, *dr = dout + (size_t)row * features;
+  float sds = 0.f, sdsx = 0.f;
+  for (int c = lane; c < features; c += 64) {
+    const float xh = (xr[c] - mean) * rstd, ds = dr[c] * (gamma ? gamma[c] : 1.f);
+    sds += ds;
+    sdsx += ds * xh;
+  }
+  const float sum_ds = wave_sum(sds), sum_dsx = wave_sum(sdsx);
+  const float f = (float)features, k = rstd / f;
+  float *gr = grad_x + (size_t)row * features;
+  for (int c = lane; c < features; c += 64) {
+    const float xh = (xr[c] - mean) * rstd, ds = dr[c] * (gamma ? gamma[c] : 1.f);
+    gr[c] = k * (f * ds - sum_ds - xh * sum_dsx);
+  }
+}
+
+// ------------------------------------------------------------- column sums
+// Sums over the rows of a [rows, cols] row-major matrix g, 64 columns per
+// workgroup of 1024 threads: lane l of wave w adds rows r = 4w + l/16 + 64k
+// (k = 0, 1, ...) of columns 4(l%16) .. +3 into float4 registers in
+// increasing k, then the 64 row slots are added in slot order through LDS.
+// LN (the LayerNorm parameter gradients): out0 receives the sums of
+// g * x_hat, x_hat = (x - means[r]) * rstds[r], and out1 those of g;
+// otherwise out0 receives the sums of g (the bias gradient). accumulate:
+// out += sums, else out = sums. cols % 4 == 0 and 16-byte aligned rows.
+template <bool LN>
+__global__ __launch_bounds__(1024) void colsum_vec_kernel(const float *__restrict__ g, const float *__restrict__ x,
+                                                          const float *__restrict__ means,
+                                                          const float *__restrict__ rstds, float *__restrict__ out0,
+                                                          float *__restrict__ out1, int rows, int cols,
+                                                          int accumulate) {
+  constexpr int kPlanes = LN ? 2 : 1;
+  __shared__ float4 part[kPlanes][64][16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int slot = 4 * w + (lane >> 4);
+  const int c4 = lane & 15;
+  const int col = blockIdx.x * 64 + 4 * c4;
+  float4 a0 = splat4(0.f), a1 = splat4(0.f);
+  if (col < cols) {
+#pragma unroll 4
+    for (int r = slot; r < rows; r += 64) {
+      const float4 gv = *reinterpret_cast<const float4 *>(g + (size_t)r * cols + col);
+      if constexpr (LN) {
+        const float4 xv = *reinterpret_cast<const float4 *>(x + (size_t)r * cols + col);
+        const float mu = means[r], rs = rstds[r];
+        a0.x += gv.x * ((xv.x - mu) * rs);
+        a0.y += gv.y * ((xv.y - mu) * rs);
+        a0.z += gv.z * ((xv.z - mu) * rs);
+        a0.w += gv.w * ((xv.w - mu) * rs);
+        a1.x += gv.x;
+        a1.y += gv.y;
+        a1.z += gv.z;
+        a1.w += gv.w;
+      } else {
+        a0.x += gv.x;
+        a0.y += gv.y;
+        a0.z += gv.z;
+        a0.w += gv.w;
+      }
+    }
+  }
+  part[0][slot][c4] = a0;
+  if constexpr (LN) part[kPlanes - 1][slot][c4] = a1;
+  __syncthreads();
+  if (tid < 64 * kPlanes) {
+    const int plane = tid >> 6, t = tid & 63;
+    const int c = blockIdx.x * 64 + t;
+    float *o = plane ? out1 : out0;
+    if (c < cols && o != nullptr) {
+      const float *p = reinterpret_cast<const float *>(&part[plane][0][0]);
+      float s = 0.f;
+      for (int k = 0; k < 64; ++k) s += p[k * 64 + t];
+      o[c] = accumulate ? o[c] + s : s;
+    }
+  }
+}
+
+// Any width and 4-byte alignment: one thread per column, rows in order.
+template <bool LN>
+__global__ __launch_bounds__(256) void colsum_generic_kernel(const float *__restrict__ g, const float *__restrict__ x,
+                                                             const float *__restrict__ means,
+                                                             const float *__restrict__ rstds, float *__restrict__ out0,
+                                                             float *__restrict__ out1, int rows, int cols,
+                                                             int accumulate) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float s0 = 0.f, s1 = 0.f;
+  for (int r = 0; r < rows; ++r) {
+    const float gv = g[(size_t)r * cols + c];
+    if constexpr (LN) {
+      s0 += gv * ((x[(size_t)r * cols + c] - means[r]) * rstds[r]);
+      s1 += gv;
+    } else {
+      s0 += gv;
+    }
+  }
+  if (out0) out0[c] = accumulate ? out0[c] + s0 : s0;
+  if constexpr (LN) {
+    if (out1) out1[c] = accumulate ? out1[c] + s1 : s1;
+  }
+}
+
+// ------------------------------------------------------------------- GELU
+__device__ __forceinline__ float gelu_f(float v) {
+  return 0.5f * v * (1.f + tanhf(kGeluK0 * (v + kGeluK1 * v * v * v)));
+}
+__device__ __forceinline__ float gelu_grad(float go, float v) {
+  const float t = tanhf(kGeluK0 * (v + kGeluK1 * v * v * v));
+  const float d_inner = kGeluK0 * (1.f + 3.f * kGeluK1 * v * v);
+  return go * (0.5f * (1.f + t) + 0.5f * v * (1.f - t * t) * d_inner);
+}
+
+// out = gelu(x) (BWD: out = go * gelu'(x)); grid-stride over float4 groups
+// when every pointer is 16-byte aligned, the n % 4 tail by the first threads.
+template <bool BWD>
+__global__ __launch_bounds__(256) void gelu_kernel(const float *__restrict__ go, const float *__restrict__ x,
+                                                   float *__restrict__ out, size_t n, int vec) {
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  size_t done = 0;
+  if (vec) {
+    const size_t n4 = n / 4;
+    for (size_t i = tid; i < n4; i += stride) {
+      const float4 v = reinterpret_cast<const float4 *>(x)[i];
+      float4 r;
+      if constexpr (BWD) {
+        const float4 gv = reinterpret_cast<const float4 *>(go)[i];
+        r = make_float4(gelu_grad(gv.x, v.x), gelu_grad(gv.y, v.y), gelu_grad(gv.z, v.z), gelu_grad(gv.w, v.w));
+      } else {
+        r = make_float4(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
+      }
+      reinterpret_cast<float4 *>(out)[i] = r;
+    }
+    done = n4 * 4;
+  }
+  for (size_t i = done + tid; i < n; i += stride) {
+    if constexpr (BWD)
+      out[i] = gelu_grad(go[i], x[i]);
+    else
+      out[i] = gelu_f(x[i]);
+  }
+}
+
+// ------------------------------------------------------------------ AdamW
+// matmul.cu:285-339: m = b1 m + (1-b1) g, v = b2 v + (1-b2) g^2,
+// p = p (1 - lr wd) - lr m_hat / (sqrt(v_hat) + eps).
+__device__ __forceinline__ void adamw1(float &p, float &m, float &v, float g, float lr, float b1, float b2,
+                                       float eps, float decay, float bc1, float bc2) {
+  m = b1 * m + (1.f - b1) * g;
+  v = b2 * v + (1.f - b2) * (g * g);
+  p = p * decay - lr * (m / bc1) / (sqrtf(v / bc2) + eps);
+}
+
+// step != nullptr: the bias corrections come from t = *step + 1 on the device.
+__global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float *__restrict__ m,
+                                                    float *__restrict__ v, const float *__restrict__ g, size_t n,
+                                                    float lr, float b1, float b2, float eps, float wd, float bc1,
+                                                    float bc2, const float *__restrict__ step, int vec) {
+  if (step != nullptr) {
+    const float t = *step + 1.f;
+    bc1 = 1.f - powf(b1, t);
+    bc2 = 1.f - powf(b2, t);
+  }
+  const float decay = 1.f - lr * wd;
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  size_t done = 0;
+  if (vec) {
+    const size_t n4 = n / 4;
+    for (size_t i = tid; i < n4; i += stride) {
+      float4 pp = reinterpret_cast<float4 *>(p)[i], mm = reinterpret_cast<float4 *>(m)[i];
+      float4 vv = reinterpret_cast<float4 *>(v)[i];
+      const float4 gg = reinterpret_cast<const float4 *>(g)[i];
+      adamw1(pp.x, mm.x, vv.x, gg.x, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp.y, mm.y, vv.y, gg.y, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp.z, mm.z, vv.z, gg.z, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp.w, mm.w, vv.w, gg.w, lr, b1, b2, eps, decay, bc1, bc2);
+      reinterpret_cast<float4 *>(p)[i] = pp;
+      reinterpret_cast<float4 *>(m)[i] = mm;
+      reinterpret_cast<float4 *>(v)[i] = vv;
+    }
+    done = n4 * 4;
+  }
+  for (size_t i = done + tid; i < n; i += stride) adamw1(p[i], m[i], v[i], g[i], lr, b1, b2, eps, decay, bc1, bc2);
+}
+
+__global__ void step_advance_kernel(float *step) {
+  if (threadIdx.x == 0) *step += 1.f;
+}
+
+// ------------------------------------------------------------------- host
+bool al(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int launched(const char *fn) {
+  const hipError_t err = hipGetLastError();
+  if (err == hipSuccess) return DFATTN_OK;
+  return record_error(DFATTN_ERR_HIP, std::string(fn) + ": " + hipGetErrorString(err));
+}
+
+int check_ptrs(const char *fn, std::initializer_list<const void *> required,
+               std::initializer_list<const void *> optional) {
+  for (const void *p : required)
+    if (p == nullptr) return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  for (const void *p : required)
+    if (!al(p, 4)) return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": pointer not 4-byte aligned");
+  for (const void *p : optional)
+    if (p != nullptr && !al(p, 4))
+      return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": pointer not 4-byte aligned");
+  return DFATTN_OK;
+}
+
+int check_dims(const char *fn, uint32_t rows, uint32_t cols) {
+  if (cols == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": features must be >= 1");
+  if (rows > (uint32_t)INT_MAX || cols > (uint32_t)INT_MAX)
+    return record_error(DFATTN_ERR_OVERFLOW, std::string(fn) + ": shape is too large");
+  return DFATTN_OK;
+}
+
+// Grid of a grid-stride elementwise kernel: 256 threads, four values each.
+unsigned elementwise_blocks(size_t n) {
+  const size_t b = (n / 4 + 255) / 256;
+  return (unsigned)(b < 1 ? 1 : (b > 4096 ? 4096 : b));
+}
+
+template <int V>
+void launch_ln_fwd_v(const float *x, const float *gamma, const float *beta, float *out, float *means, float *rstds,
+                     int batch, int features, hipStream_t stream) {
+  hipLaunchKernelGGL(ln_fwd_vec_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, x, gamma, beta, out, means,
+                     rstds, batch, features);
+}
+
+template <int V>
+void launch_ln_dx_v(const float *dout, const float *x, const float *gamma, const float *means, const float *rstds,
+                    float *grad_x, int batch, int features, hipStream_t stream) {
+  hipLaunchKernelGGL(ln_bwd_dx_vec_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, dout, x, gamma, means,
+                     rstds, grad_x, batch, features);
+}
+
+// The register-resident row path: features % 4 == 0, at most 1024, 16-byte
+// aligned tensors.
+bool ln_vec(uint32_t features, std::initializer_list<const void *> ptrs) {
+  if (features % 4 != 0 || features > 1024) return false;
+  for (const void *p : ptrs)
+    if (p != nullptr && !al(p, 16)) return false;
+  return true;
+}
+
+template <bool LN>
+void launch_colsum(const float *g, const float *x, const float *means, const float *rstds, float *out0, float *out1,
+                   int rows, int cols, int accumulate, bool vec, hipStream_t stream) {
+  if (vec)
+    hipLaunchKernelGGL(colsum_vec_kernel<LN>, dim3((cols + 63) / 64), dim3(1024), 0, stream, g, x, means, rstds,
+                       out0, out1, rows, cols, accumulate);
+  else
+    hipLaunchKernelGGL(colsum_generic_kernel<LN>, dim3((cols + 255) / 256), dim3(256), 0, stream, g, x, means,
+                       rstds, out0, out1, rows, cols, accumulate);
+}
+
+}  // namespace
+}  // namespace dfattn
+
+using namespace dfattn;
+
+extern "C" int dfgpt2_layernorm_forward(const float *x, const float *gamma, const float *beta, float *out,
+                                        float *means, float *rstds, uint32_t batch, uint32_t features,
+                                        hipStream_t stream) {
+  const char *fn = "dfgpt2_layernorm_forward";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;  // no rows: nothing to read or write
+  if (int st = check_ptrs(fn, {x, out}, {gamma, beta, means, rstds}); st != DFATTN_OK) return st;
+  const int b = (int)batch, f = (int)features;
+  if (ln_vec(features, {x, out, gamma, beta})) {
+    switch ((f / 4 + 63) / 64) {
+      case 1: launch_ln_fwd_v<1>(x, gamma, beta, out, means, rstds, b, f, stream); break;
+      case 2: launch_ln_fwd_v<2>(x, gamma, beta, out, means, rstds, b, f, stream); break;
+      case 3: launch_ln_fwd_v<3>(x, gamma, beta, out, means, rstds, b, f, stream); break;
+      default: launch_ln_fwd_v<4>(x, gamma, beta, out, means, rstds, b, f, stream); break;
+    }
+  } else {
+    hipLaunchKernelGGL(ln_fwd_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, x, gamma, beta, out, means,
+                       rstds, b, f);
+  }
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_layernorm_backward(const float *grad_out, const float *x, const float *gamma,
+                                         const float *means, const float *rstds, float *grad_x, float *grad_gamma,
+                                         float *grad_beta, uint32_t batch, uint32_t features, hipStream_t stream) {
+  const char *fn = "dfgpt2_layernorm_backward";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;  // no rows: grad_x is empty and nothing is added
+  if (int st = check_ptrs(fn, {grad_out, x, means, rstds, grad_x}, {gamma, grad_gamma, grad_beta}); st != DFATTN_OK)
+    return st;
+  const int b = (int)batch, f = (int)features;
+  if (ln_vec(features, {grad_out, x, gamma, grad_x})) {
+    switch ((f / 4 + 63) / 64) {
+      case 1: launch_ln_dx_v<1>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
+      case 2: launch_ln_dx_v<2>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
+      case 3: launch_ln_dx_v<3>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
+      default: launch_ln_dx_v<4>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
+    }
+  } else {
+    hipLaunchKernelGGL(ln_bwd_dx_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, grad_out, x, gamma, means,
+                       rstds, grad_x, b, f);
+  }
+  if (int st = launched(fn); st != DFATTN_OK) return st;
+  if (grad_gamma == nullptr && grad_beta == nullptr) return DFATTN_OK;
+  const bool vec = f % 4 == 0 && al(grad_out, 16) && al(x, 16);
+  launch_colsum<true>(grad_out, x, means, rstds, grad_gamma, grad_beta, b, f, 1, vec, stream);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream) {
+  const char *fn = "dfgpt2_gelu_forward";
+  if (n == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {x, out}, {}); st != DFATTN_OK) return st;
+  hipLaunchKernelGGL(gelu_kernel<false>, dim3(elementwise_blocks(n)), dim3(256), 0, stream, nullptr, x, out, n,
+                     (al(x, 16) && al(out, 16)) ? 1 : 0);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_gelu_backward(const float *grad_out, const float *x, float *grad_x, size_t n,
+                                    hipStream_t stream) {
+  const char *fn = "dfgpt2_gelu_backward";
+  if (n == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {grad_out, x, grad_x}, {}); st != DFATTN_OK) return st;
+  hipLaunchKernelGGL(gelu_kernel<true>, dim3(elementwise_blocks(n)), dim3(256), 0, stream, grad_out, x, grad_x, n,
+                     (al(grad_out, 16) && al(x, 16) && al(grad_x, 16)) ? 1 : 0);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch,
+                                       uint32_t out_features, int accumulate, hipStream_t stream) {
+  const char *fn = "dfgpt2_linear_grad_bias";
+  // No rows: grad_out may be empty (NULL) and the sums are zero.
+  if (int st = check_ptrs(fn, {grad_bias}, {grad_out}); st != DFATTN_OK) return st;
+  if (batch > 0 && grad_out == nullptr) return record_error(DFATTN_ERR_NULL_POINTER, std::string(fn) + ": null pointer");
+  if (int st = check_dims(fn, batch, out_features); st != DFATTN_OK) return st;
+  const bool vec = out_features % 4 == 0 && al(grad_out, 16);
+  launch_colsum<false>(grad_out, nullptr, nullptr, nullptr, grad_bias, nullptr, (int)batch, (int)out_features,
+                       accumulate ? 1 : 0, vec, stream);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_adamw_update(float *parameter, float *first_moment, float *second_moment,
+                                   const float *gradient, size_t n, float lr, float beta1, float beta2, float eps,
+                                   float weight_decay, float *step, hipStream_t stream) {
+  const char *fn = "dfgpt2_adamw_update";
+  if (int st = check_ptrs(fn, {parameter, first_moment, second_moment, gradient, step}, {}); st != DFATTN_OK)
+    return st;
+  const int vec = (al(parameter, 16) && al(first_moment, 16) && al(second_moment, 16) && al(gradient, 16)) ? 1 : 0;
+  if (n > 0) {
+    hipLaunchKernelGGL(adamw_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, stream, parameter, first_moment,
+                       second_moment, gradient, n, lr, beta1, beta2, eps, weight_decay, 1.f, 1.f, step, vec);
+    if (int st = launched(fn); st != DFATTN_OK) return st;
+  }
+  hipLaunchKernelGGL(step_advance_kernel, dim3(1), dim3(64), 0, stream, step);
+  return launched(fn);
+}
+
+// ------------------------------------------------- the reference's symbols
+extern "C" void launch_layernorm(const float *x, const float *gamma, const float *beta, float *out, float *means,
+                                 float *rstds, uint32_t batch, uint32_t features) {
+  mark_pending(dfgpt2_layernorm_forward(x, gamma, beta, out, means, rstds, batch, features, nullptr));
+}
+
+extern "C" void launch_layernorm_backward(const float *grad_out, const float *x, const float *gamma,
+                                          const float *means, const float *rstds, float *grad_x, float *grad_gamma,
+                                          float *grad_beta, uint32_t batch, uint32_t features) {
+  mark_pending(dfgpt2_layernorm_backward(grad_out, x, gamma, means, rstds, grad_x, grad_gamma, grad_beta, batch,
+                                         features, nullptr));
+}
+
+extern "C" void launch_gelu(const float *x, float *out, uint32_t n) {
+  mark_pending(dfgpt2_gelu_forward(x, out, n, nullptr));
+}
+
+extern "C" void launch_gelu_backward(const float *grad_out, const float *x, float *grad_x, uint32_t n) {
+  mark_pending(dfgpt2_gelu_backward(grad_out, x, grad_x, n, nullptr));
+}
+
+extern "C" void launch_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch,
+                                        uint32_t out_features) {
+  mark_pending(dfgpt2_linear_grad_bias(grad_out, grad_bias, batch, out_features, 0, nullptr));
+}
+
+extern "C" void launch_adamw_update(float *parameter, float *first_moment, float *second_moment,
+                                    const float *gradient, uint32_t n, float lr, float beta1, float beta2, float eps,
+                                    float weight_decay, float bias_correction1, float bias_correction2) {
+  const char *fn = "launch_adamw_update";
+  int st = check_ptrs(fn, {parameter, first_moment, second_moment, gradient}, {});
+  if (st == DFATTN_OK && n > 0) {
+    const int vec = (al(parameter, 16) && al(first_moment, 16) && al(second_moment, 16) && al(gradient, 16)) ? 1 : 0;
+    hipLaunchKernelGGL(adamw_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, nullptr, parameter, first_moment,
+                       second_moment, gradient, (size_t)n, lr, beta1, beta2, eps, weight_decay, bias_correction1,
+                       bias_correction2, nullptr, vec);
+    st = launched(fn);
+  }
+  mark_pending(st);
+}

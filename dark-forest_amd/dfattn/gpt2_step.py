@@ -18,9 +18,11 @@ Mirrors the reference's static engine step (darkforest-core/src/engine/static_gp
   FusedCausalAttention, which keeps the forward's O and logsumexp for the
   backward.
 
-Everything except attention is plain PyTorch in fp32 (GEMMs through
-hipBLASLt/rocBLAS); it is the measurement harness of the attention path, not
-a reimplementation of the reference's other kernels. `attention="sdpa"`
+On the GPU the step's other kernels are this library's too (dfattn.ops, include/dfgpt2.h):
+LayerNorm forward and backward, tanh GELU, the linear layers' bias gradients and AdamW over one
+arena holding every weight, gradient and moment (the engine's single allocation), all fp32; the
+GEMMs are hipBLASLt fp32. On the CPU (the checkpoint tests' twin) the same model runs on PyTorch's
+operators and optimizer. `attention="sdpa"`
 swaps in torch's scaled_dot_product_attention (the reference's own parity
 comparator, scripts/verify_loss_parity.py:58) for loss-parity checks.
 """
@@ -31,6 +33,7 @@ import struct
 import time
 
 from . import FusedCausalAttention
+from . import ops as _ops
 
 
 def _torch():
@@ -84,21 +87,33 @@ class StaticGPT2:
         # The engine keeps its hyper-parameters as f32 (static_gpt2.rs:518-521), which its checkpoint
         # footer stores; holding the same f32 values makes a resumed run continue bit for bit.
         f32 = lambda x: struct.unpack("<f", struct.pack("<f", x))[0]  # noqa: E731
-        # On the GPU the update is one fused kernel per parameter group (the engine's update is one
-        # kernel per tensor, lib.rs:1755-1788); the multi-pass foreach update costs about 2.8 ms more
-        # per GPT-2 small step. capturable: AdamW keeps its step counts on the device, so a step can
-        # be recorded into a graph.
-        self.opt = torch.optim.AdamW(self.parameters(), lr=f32(lr), betas=(f32(0.9), f32(0.95)), eps=f32(1e-8),
-                                     weight_decay=f32(0.1), fused=self.device.type == "cuda",
-                                     capturable=capturable)
+        # On the GPU: one arena for weights, gradients and moments, the AdamW update in one launch
+        # (the engine's update is one kernel per tensor, lib.rs:1755-1788), the step count on the
+        # device, so a step can always be recorded into a graph. On the CPU: torch's AdamW.
+        self.native = self.device.type == "cuda"
+        hp = dict(lr=f32(lr), betas=(f32(0.9), f32(0.95)), eps=f32(1e-8), weight_decay=f32(0.1))
+        if self.native:
+            arena = _ops.ParamArena(self.parameters(), self.device)
+            self._rebind(arena.adopt(self.parameters()))
+            self.opt = _ops.ArenaAdamW(arena, self.parameters(), **hp)
+        else:
+            self.opt = torch.optim.AdamW(self.parameters(), **hp, capturable=capturable)
         self._graph = None
-        self.pos_idx = torch.arange(seq_len, device=self.device)
 
     def parameters(self):
         ps = [self.tok_emb, self.pos_emb]
         for lw in self.layers:
             ps += list(lw.values())
         return ps + [self.ln_f_g, self.ln_f_b, self.lm_head]
+
+    def _rebind(self, tensors):
+        """Replace the parameters (in parameters() order) with `tensors`."""
+        it = iter(tensors)
+        self.tok_emb, self.pos_emb = next(it), next(it)
+        for lw in self.layers:
+            for key in lw:
+                lw[key] = next(it)
+        self.ln_f_g, self.ln_f_b, self.lm_head = next(it), next(it), next(it)
 
     def load_state(self, other: "StaticGPT2"):
         """Copy another instance's weights (the parity harness loads identical weights into both)."""
@@ -120,17 +135,28 @@ class StaticGPT2:
     def loss(self, tokens, targets):
         """Mean cross-entropy of one sequence (static_gpt2.rs:1386-1418)."""
         F = _torch().nn.functional
-        x = self.tok_emb[tokens] + self.pos_emb[self.pos_idx]
+        if self.native:
+            # the parameter gradients go straight into the arena (ops: direct accumulation)
+            ln = lambda t, g, b: _ops.layer_norm(t, g, b, direct=True)  # noqa: E731
+            lin = lambda t, w, b=None: _ops.linear(t, w, b, direct=True)  # noqa: E731
+            gelu = _ops.gelu
+            x = _ops.embedding(self.tok_emb, tokens, direct=True)
+        else:
+            d = self.d_model
+            ln = lambda t, g, b: F.layer_norm(t, (d,), g, b, 1e-5)  # noqa: E731
+            lin, gelu = F.linear, lambda t: F.gelu(t, approximate="tanh")  # noqa: E731
+            x = self.tok_emb[tokens]
+        x = x + self.pos_emb[:tokens.shape[0]]
         for lw in self.layers:
-            h = F.layer_norm(x, (self.d_model,), lw["ln1_g"], lw["ln1_b"], 1e-5)
-            q = F.linear(h, lw["wq"], lw["bq"])
-            k = F.linear(h, lw["wk"], lw["bk"])
-            v = F.linear(h, lw["wv"], lw["bv"])
-            x = x + F.linear(self._attention(q, k, v), lw["wo"], lw["bo"])
-            h = F.layer_norm(x, (self.d_model,), lw["ln2_g"], lw["ln2_b"], 1e-5)
-            x = x + F.linear(F.gelu(F.linear(h, lw["w1"], lw["b1"]), approximate="tanh"), lw["w2"], lw["b2"])
-        h = F.layer_norm(x, (self.d_model,), self.ln_f_g, self.ln_f_b, 1e-5)
-        return F.cross_entropy(F.linear(h, self.lm_head), targets)
+            h = ln(x, lw["ln1_g"], lw["ln1_b"])
+            q = lin(h, lw["wq"], lw["bq"])
+            k = lin(h, lw["wk"], lw["bk"])
+            v = lin(h, lw["wv"], lw["bv"])
+            x = x + lin(self._attention(q, k, v), lw["wo"], lw["bo"])
+            h = ln(x, lw["ln2_g"], lw["ln2_b"])
+            x = x + lin(gelu(lin(h, lw["w1"], lw["b1"])), lw["w2"], lw["b2"])
+        h = ln(x, self.ln_f_g, self.ln_f_b)
+        return F.cross_entropy(lin(h, self.lm_head), targets)
 
     def step(self, tokens, targets):
         """One training step: forward, loss, backward, AdamW. Returns the loss tensor (not synchronised)."""
@@ -145,7 +171,8 @@ class StaticGPT2:
         """Record one whole training step into a HIP graph (the engine replays a captured step too,
         static_gpt2.rs graph_exec) after `warmup` eager steps on a side stream, which allocate the
         optimizer state and the autograd buffers. Returns the static loss tensor every replay() updates.
-        Needs capturable=True. The batch is copied into static buffers; set_batch() changes it."""
+        On the CPU it needs capturable=True (the GPU optimizer always keeps its step count on the
+        device). The batch is copied into static buffers; set_batch() changes it."""
         torch = _torch()
         if not self.opt.param_groups[0]["capturable"]:
             raise ValueError("StaticGPT2.capture needs capturable=True")
@@ -181,25 +208,32 @@ def synthetic_batch(vocab_size, seq_len, seed, device):
     return ids[:-1].to(device), ids[1:].to(device)
 
 
-def time_steps(model, steps=10, warmup=3, seed=1):
+def time_steps(model, steps=10, warmup=3, seed=1, graph=False):
     """Median and all per-step wall times (ms) of full training steps, device-synchronised per step.
 
     The methodology of the reference's step benchmark (benchmark/bench_darkforest_e2e.py:116-133:
-    warmup, then timed steps each ending in a device sync), with seeded tokens.
+    warmup, then timed steps each ending in a device sync), with seeded tokens. graph=True records
+    one step into a HIP graph after the warmup steps (StaticGPT2.capture) and times its replays: the
+    same kernels without the Python dispatch between them, like the engine's host-side loop.
     """
     torch = _torch()
     tokens, targets = synthetic_batch(model.vocab_size, model.seq_len, seed, model.device)
     losses = []
-    for _ in range(warmup):
-        losses.append(float(model.step(tokens, targets)))
+    if graph:
+        static_loss = model.capture(tokens, targets, warmup=warmup)
+        run = model.replay
+    else:
+        for _ in range(warmup):
+            losses.append(float(model.step(tokens, targets)))
+        run = lambda: model.step(tokens, targets)  # noqa: E731
     torch.cuda.synchronize()
     times = []
     for _ in range(steps):
         t0 = time.perf_counter()
-        loss = model.step(tokens, targets)
+        loss = run()
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
-        losses.append(float(loss))
+        losses.append(float(static_loss if graph else loss))
     ordered = sorted(times)
     return {"median_ms": ordered[len(ordered) // 2], "min_ms": ordered[0], "times_ms": times, "losses": losses,
             "peak_mem_mb": torch.cuda.max_memory_allocated() / 2 ** 20}

@@ -1,0 +1,63 @@
+/* dfgpt2.h — C ABI of the GPT-2 step's non-attention kernels in libdfattn.so (gfx950).
+ *
+ * The reference engine's training step (darkforest-core/src/engine/static_gpt2.rs:1375-1696)
+ * calls these CUDA launchers around its attention; the six reference symbols below keep their
+ * signatures and semantics (null stream, void return, argument errors reported by
+ * darkforest_sync, declared in dfattn.h). The dfgpt2_* entry points are the same kernels on an
+ * explicit stream with a dfattn_status return. Every reduction adds in a fixed order (no
+ * floating-point atomics), so results are bitwise reproducible from run to run.
+ */
+#ifndef DFGPT2_H
+#define DFGPT2_H
+
+#include "dfattn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* darkforest-cuda/kernels/layernorm.cu:97. out = (x - mean) * rstd * gamma + beta per row of
+ * [batch, features], eps 1e-5; gamma / beta NULL mean 1 / 0; means / rstds ([batch]) may be NULL. */
+void launch_layernorm(const float *x, const float *gamma, const float *beta, float *out, float *means,
+                      float *rstds, uint32_t batch, uint32_t features);
+/* layernorm.cu:187. grad_x overwritten; grad_gamma and grad_beta ([features], each may be NULL)
+ * ACCUMULATE the column sums of grad_out * x_hat and of grad_out (the reference adds them with
+ * atomics), so the caller zeroes them first. */
+void launch_layernorm_backward(const float *grad_out, const float *x, const float *gamma, const float *means,
+                               const float *rstds, float *grad_x, float *grad_gamma, float *grad_beta,
+                               uint32_t batch, uint32_t features);
+/* elementwise.cu:195, 217: tanh GELU, 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))). */
+void launch_gelu(const float *x, float *out, uint32_t n);
+void launch_gelu_backward(const float *grad_out, const float *x, float *grad_x, uint32_t n);
+/* matmul.cu:240: grad_bias[j] = sum over rows of grad_out[row, j] (overwritten). */
+void launch_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch, uint32_t out_features);
+/* matmul.cu:341: m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;
+ * p = p (1 - lr wd) - lr (m / bc1) / (sqrt(v / bc2) + eps), elementwise over n values. */
+void launch_adamw_update(float *parameter, float *first_moment, float *second_moment, const float *gradient,
+                         uint32_t n, float lr, float beta1, float beta2, float eps, float weight_decay,
+                         float bias_correction1, float bias_correction2);
+
+/* Stream variants. Pointers must be 4-byte aligned; 16-byte aligned rows with features % 4 == 0
+ * take the vectorised kernels. batch == 0 or n == 0 is a no-op (the bias gradient is then zero), and
+ * the pointers of an empty tensor may be NULL. */
+int dfgpt2_layernorm_forward(const float *x, const float *gamma, const float *beta, float *out, float *means,
+                             float *rstds, uint32_t batch, uint32_t features, hipStream_t stream);
+int dfgpt2_layernorm_backward(const float *grad_out, const float *x, const float *gamma, const float *means,
+                              const float *rstds, float *grad_x, float *grad_gamma, float *grad_beta,
+                              uint32_t batch, uint32_t features, hipStream_t stream);
+int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream);
+int dfgpt2_gelu_backward(const float *grad_out, const float *x, float *grad_x, size_t n, hipStream_t stream);
+/* accumulate != 0: grad_bias += column sums (else overwritten). */
+int dfgpt2_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch, uint32_t out_features,
+                            int accumulate, hipStream_t stream);
+/* The AdamW update with the step count on the device (a float, as PyTorch keeps it): the kernel
+ * takes t = *step + 1 for the bias corrections 1 - beta^t, then *step becomes t. Nothing about the
+ * step is read on the host, so a captured graph stays correct on replay. */
+int dfgpt2_adamw_update(float *parameter, float *first_moment, float *second_moment, const float *gradient,
+                        size_t n, float lr, float beta1, float beta2, float eps, float weight_decay, float *step,
+                        hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DFGPT2_H */

@@ -1,0 +1,75 @@
+"""The GPT-2 step ops' C ABI (include/dfgpt2.h) on the CPU: every declared symbol is exported and
+typed, and bad arguments are rejected on the host before any HIP call (no GPU needed)."""
+import ctypes
+import os
+
+import pytest
+
+import dfattn
+from conftest import ROOT
+from dfattn import ops
+from test_abi import declared_functions
+
+HEADER = os.path.join(ROOT, "include", "dfgpt2.h")
+# dfattn_status codes (include/dfattn.h)
+OK, ERR_NULL, ERR_MISALIGNED, ERR_SHAPE, ERR_OVERFLOW = dfattn.DFATTN_OK, -1, -2, -3, -5
+
+
+def test_every_declared_symbol_is_exported_and_typed():
+    lib = ops.ops_lib()
+    declared = declared_functions(HEADER)
+    assert "launch_layernorm" in declared and "dfgpt2_adamw_update" in declared
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in dfgpt2.h but not exported"
+    assert sorted(ops.SYMBOLS) == declared
+
+
+def _status(fn, *args):
+    return getattr(ops.ops_lib(), fn)(*args)
+
+
+BUF = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+ODD = ctypes.c_void_p(0x1002)
+
+
+@pytest.mark.parametrize("fn,args,status", [
+    ("dfgpt2_layernorm_forward", (None, None, None, BUF, None, None, 4, 8, None), ERR_NULL),
+    ("dfgpt2_layernorm_forward", (ODD, None, None, BUF, None, None, 4, 8, None), ERR_MISALIGNED),
+    ("dfgpt2_layernorm_forward", (BUF, ODD, None, BUF, None, None, 4, 8, None), ERR_MISALIGNED),
+    ("dfgpt2_layernorm_forward", (BUF, None, None, BUF, None, None, 4, 0, None), ERR_SHAPE),
+    ("dfgpt2_layernorm_forward", (BUF, None, None, BUF, None, None, 2**31, 8, None), ERR_OVERFLOW),
+    ("dfgpt2_layernorm_forward", (BUF, None, None, BUF, None, None, 0, 8, None), OK),
+    ("dfgpt2_layernorm_backward", (BUF, BUF, None, None, BUF, BUF, None, None, 4, 8, None),
+     ERR_NULL),
+    ("dfgpt2_layernorm_backward", (BUF, BUF, None, BUF, BUF, BUF, ODD, None, 4, 8, None),
+     ERR_MISALIGNED),
+    ("dfgpt2_gelu_forward", (BUF, None, 16, None), ERR_NULL),
+    ("dfgpt2_gelu_forward", (BUF, BUF, 0, None), OK),
+    ("dfgpt2_gelu_forward", (None, None, 0, None), OK),
+    ("dfgpt2_layernorm_backward", (None,) * 8 + (0, 8, None), OK),
+    ("dfgpt2_gelu_backward", (BUF, ODD, BUF, 16, None), ERR_MISALIGNED),
+    ("dfgpt2_linear_grad_bias", (BUF, None, 4, 8, 0, None), ERR_NULL),
+    ("dfgpt2_linear_grad_bias", (BUF, BUF, 4, 0, 0, None), ERR_SHAPE),
+    ("dfgpt2_adamw_update", (BUF, BUF, BUF, BUF, 16, 1e-3, 0.9, 0.95, 1e-8, 0.1, None, None),
+     ERR_NULL),
+])
+def test_argument_errors_are_caught_on_the_host(fn, args, status):
+    ops.ops_lib().dfattn_clear_error()
+    assert _status(fn, *args) == status
+    if status != OK:
+        assert ops.ops_lib().dfattn_last_error() == status
+    ops.ops_lib().dfattn_clear_error()
+
+
+def test_reference_launcher_records_error_for_darkforest_sync():
+    """The reference symbols return void: an argument error is kept for darkforest_sync (which
+    aborts on it, in a subprocess in test_abi) and nothing is launched."""
+    lib = ops.ops_lib()
+    lib.dfattn_clear_error()
+    lib.launch_layernorm(None, None, None, None, None, None, 4, 8)
+    assert lib.dfattn_last_error() == ERR_NULL
+    assert "dfgpt2_layernorm_forward" in lib.dfattn_last_error_message().decode()
+    lib.dfattn_clear_error()
+    lib.launch_adamw_update(None, BUF, BUF, BUF, 16, 1e-3, 0.9, 0.95, 1e-8, 0.1, 0.1, 0.05)
+    assert lib.dfattn_last_error() == ERR_NULL
+    lib.dfattn_clear_error()

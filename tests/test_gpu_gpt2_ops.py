@@ -1,0 +1,184 @@
+"""The GPT-2 step's non-attention kernels (include/dfgpt2.h) on the GPU against PyTorch fp32
+operators of the same maths (float64 for AdamW), plus bitwise reproducibility of the reductions and
+the reference launchers (null stream) against the stream entry points."""
+import ctypes
+
+import pytest
+
+import dfattn
+from dfattn import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[gpu-gpt2-ops] {msg}", flush=True)
+
+
+def P(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def close(a, b, rtol, atol, what):
+    import torch
+
+    err = (a - b).abs().max().item()
+    ok = torch.allclose(a, b, rtol=rtol, atol=atol)
+    say(f"{what}: max abs err {err:.3e}")
+    assert ok, f"{what}: max abs err {err}"
+
+
+# (rows, features): the GPT-2 width (register path), a width that is not a multiple of 4 and one
+# above the register path's 1024 (generic paths), a single row
+LN_SHAPES = [(1024, 768), (37, 130), (64, 2048), (1, 768)]
+
+
+@pytest.mark.parametrize("rows,f", LN_SHAPES)
+@pytest.mark.parametrize("affine", [True, False])
+def test_layernorm_forward_and_backward_match_torch(device, rows, f, affine):
+    import torch
+
+    say(f"layernorm rows={rows} f={f} affine={affine}")
+    g = torch.Generator(device="cpu").manual_seed(rows * 31 + f)
+    x = (torch.randn(rows, f, generator=g) * 3 + 0.5).to(device)
+    gamma = (torch.randn(f, generator=g)).to(device) if affine else None
+    beta = (torch.randn(f, generator=g)).to(device) if affine else None
+    dy = torch.randn(rows, f, generator=g).to(device)
+    out, means, rstds = ops.layer_norm_forward(x, gamma, beta)
+    xr = x.clone().requires_grad_(True)
+    gr = gamma.clone().requires_grad_(True) if affine else None
+    br = beta.clone().requires_grad_(True) if affine else None
+    ref = torch.nn.functional.layer_norm(xr, (f,), gr, br, 1e-5)
+    close(out, ref.detach(), 1e-5, 1e-5, "out")
+    close(means, x.mean(1), 1e-5, 1e-5, "means")
+    close(rstds, (x.var(1, unbiased=False) + 1e-5).rsqrt(), 1e-5, 1e-6, "rstds")
+    ref.backward(dy)
+    gx, gg, gb = ops.layer_norm_backward(dy, x, gamma, means, rstds)
+    close(gx, xr.grad, 1e-4, 1e-5, "grad_x")
+    if affine:
+        close(gg, gr.grad, 1e-4, 1e-4 * rows ** 0.5, "grad_gamma")
+        close(gb, br.grad, 1e-4, 1e-4 * rows ** 0.5, "grad_beta")
+
+
+def test_layernorm_backward_accumulates_parameter_gradients(device):
+    """grad_gamma / grad_beta are added to, as the reference's atomics add (layernorm.cu:140-141)."""
+    import torch
+
+    rows, f = 256, 768
+    x, dy = torch.randn(rows, f, device=device), torch.randn(rows, f, device=device)
+    gamma = torch.randn(f, device=device)
+    _, means, rstds = ops.layer_norm_forward(x, gamma, None)
+    _, gg, gb = ops.layer_norm_backward(dy, x, gamma, means, rstds)
+    gx = torch.empty_like(x)
+    acc_g, acc_b = torch.full((f,), 2.0, device=device), torch.full((f,), -1.0, device=device)
+    dfattn._check(ops.ops_lib().dfgpt2_layernorm_backward(P(dy), P(x), P(gamma), P(means), P(rstds), P(gx),
+                                                          P(acc_g), P(acc_b), rows, f, None))
+    torch.cuda.synchronize()
+    assert torch.equal(acc_g, gg + 2.0) and torch.equal(acc_b, gb - 1.0)
+
+
+@pytest.mark.parametrize("rows,n", [(1024, 768), (1024, 3072), (1000, 50), (1, 768), (0, 64)])
+def test_bias_gradient_is_the_column_sum(device, rows, n):
+    import torch
+
+    say(f"bias grad rows={rows} n={n}")
+    gy = torch.randn(rows, n, device=device)
+    gb = ops.bias_grad(gy)
+    close(gb, gy.double().sum(0).float(), 0, 2e-5 * max(rows, 1) ** 0.5, "bias grad")
+    # accumulate onto an existing gradient
+    acc = torch.ones(n, device=device)
+    dfattn._check(ops.ops_lib().dfgpt2_linear_grad_bias(P(gy), P(acc), rows, n, 1, None))
+    torch.cuda.synchronize()
+    assert torch.equal(acc, gb + 1.0)
+
+
+def test_reductions_are_bitwise_reproducible(device):
+    import torch
+
+    x, dy = torch.randn(1024, 768, device=device), torch.randn(1024, 768, device=device)
+    gamma = torch.randn(768, device=device)
+    _, m, r = ops.layer_norm_forward(x, gamma, None)
+    first = ops.layer_norm_backward(dy, x, gamma, m, r) + (ops.bias_grad(dy),)
+    for _ in range(3):
+        again = ops.layer_norm_backward(dy, x, gamma, m, r) + (ops.bias_grad(dy),)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("n", [1024 * 3072, 1001, 3])
+def test_gelu_forward_and_backward_match_torch(device, n):
+    import torch
+
+    x = torch.randn(n, device=device) * 3
+    dy = torch.randn(n, device=device)
+    xr = x.clone().requires_grad_(True)
+    ref = torch.nn.functional.gelu(xr, approximate="tanh")
+    close(ops.gelu_forward(x), ref.detach(), 1e-5, 1e-6, "gelu")
+    ref.backward(dy)
+    close(ops.gelu_backward(dy, x), xr.grad, 1e-5, 1e-5, "gelu backward")
+    # misaligned (offset by one float) views take the scalar path
+    if n > 8:
+        close(ops.gelu_forward(x[1:]), ref.detach()[1:], 1e-5, 1e-6, "gelu, unaligned")
+
+
+def _adamw_ref(p, m, v, g, lr, b1, b2, eps, wd, t):
+    """matmul.cu:300-306 in float64."""
+    m = b1 * m + (1 - b1) * g
+    v = b2 * v + (1 - b2) * g * g
+    bc1, bc2 = 1 - b1 ** t, 1 - b2 ** t
+    return p * (1 - lr * wd) - lr * (m / bc1) / ((v / bc2).sqrt() + eps), m, v
+
+
+def test_adamw_matches_the_reference_update_and_counts_steps(device):
+    import torch
+
+    n = 1_000_003
+    p, g = torch.randn(n, device=device), torch.randn(n, device=device) * 1e-2
+    m, v = torch.zeros(n, device=device), torch.zeros(n, device=device)
+    step = torch.zeros(1, device=device)
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.95, 1e-8, 0.1
+    pd, md, vd = p.double(), m.double(), v.double()
+    for t in range(1, 4):
+        gt = g * t
+        dfattn._check(ops.ops_lib().dfgpt2_adamw_update(P(p), P(m), P(v), P(gt), n, lr, b1, b2, eps, wd, P(step),
+                                                        None))
+        pd, md, vd = _adamw_ref(pd, md, vd, gt.double(), lr, b1, b2, eps, wd, t)
+        torch.cuda.synchronize()
+        assert float(step) == t
+        close(p.double(), pd, 0, 1e-6, f"adamw p, step {t}")
+        close(m.double(), md, 1e-5, 1e-9, f"adamw m, step {t}")
+        close(v.double(), vd, 1e-5, 1e-12, f"adamw v, step {t}")
+
+
+def test_reference_launchers_match_the_stream_entry_points(device):
+    import torch
+
+    lib = ops.ops_lib()
+    lib.dfattn_clear_error()
+    rows, f = 333, 768
+    x, dy = torch.randn(rows, f, device=device), torch.randn(rows, f, device=device)
+    gamma, beta = torch.randn(f, device=device), torch.randn(f, device=device)
+    out, m, r = torch.empty_like(x), torch.empty(rows, device=device), torch.empty(rows, device=device)
+    gx, gg, gb = torch.empty_like(x), torch.zeros(f, device=device), torch.zeros(f, device=device)
+    bias, ge, gge = torch.empty(f, device=device), torch.empty_like(x), torch.empty_like(x)
+    lib.launch_layernorm(P(x), P(gamma), P(beta), P(out), P(m), P(r), rows, f)
+    lib.launch_layernorm_backward(P(dy), P(x), P(gamma), P(m), P(r), P(gx), P(gg), P(gb), rows, f)
+    lib.launch_linear_grad_bias(P(dy), P(bias), rows, f)
+    lib.launch_gelu(P(x), P(ge), rows * f)
+    lib.launch_gelu_backward(P(dy), P(x), P(gge), rows * f)
+    lib.darkforest_sync()
+    want_out, wm, wr = ops.layer_norm_forward(x, gamma, beta)
+    wgx, wgg, wgb = ops.layer_norm_backward(dy, x, gamma, wm, wr)
+    torch.cuda.synchronize()
+    for a, b in [(out, want_out), (m, wm), (r, wr), (gx, wgx), (gg, wgg), (gb, wgb), (bias, ops.bias_grad(dy)),
+                 (ge, ops.gelu_forward(x)), (gge, ops.gelu_backward(dy, x))]:
+        assert torch.equal(a, b)
+    # the reference AdamW takes the bias corrections from the caller
+    n = 4099
+    p, g = torch.randn(n, device=device), torch.randn(n, device=device)
+    mm, vv = torch.zeros(n, device=device), torch.zeros(n, device=device)
+    p0 = p.double()
+    lib.launch_adamw_update(P(p), P(mm), P(vv), P(g), n, 1e-3, 0.9, 0.95, 1e-8, 0.1, 1 - 0.9, 1 - 0.95)
+    lib.darkforest_sync()
+    want, _, _ = _adamw_ref(p0, 0, 0, g.double(), 1e-3, 0.9, 0.95, 1e-8, 0.1, 1)
+    close(p.double(), want, 0, 1e-6, "launch_adamw_update")
