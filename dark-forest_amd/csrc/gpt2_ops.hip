@@ -9,7 +9,7 @@
 // All of them are memory-bound (a few bytes per flop): rows are read as
 // float4 by wave64 lanes, LayerNorm keeps a row in registers (one wave per
 // row), and the column reductions (bias and LayerNorm parameter gradients)
-// give each workgroup 64 columns and a fixed summation order instead of the
+// give each workgroup 16 columns and a fixed summation order instead of the
 // reference's floating-point atomics, so every result is reproducible bit
 // for bit (AdamW's sign-sensitive update of a near-zero gradient depends on
 // that).
@@ -180,14 +180,18 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_generic_kernel(const float *__r
 }
 
 // ------------------------------------------------------------- column sums
-// Sums over the rows of a [rows, cols] row-major matrix g, 64 columns per
-// workgroup of 1024 threads: lane l of wave w adds rows r = 4w + l/16 + 64k
-// (k = 0, 1, ...) of columns 4(l%16) .. +3 into float4 registers in
-// increasing k, then the 64 row slots are added in slot order through LDS.
+// Sums over the rows of a [rows, cols] row-major matrix g, kColStrip = 16
+// columns per workgroup of 1024 threads (48 workgroups at 768 columns): lane
+// l of wave w reads columns 4(l%4) .. +3 (float4) of rows r = 16w + l/4 +
+// 256k (k = 0, 1, ...) and adds them in increasing k; the 256 row slots are
+// then added through LDS in two fixed stages (contiguous groups of slots,
+// then the groups in order), so every sum has one order and is reproducible.
 // LN (the LayerNorm parameter gradients): out0 receives the sums of
 // g * x_hat, x_hat = (x - means[r]) * rstds[r], and out1 those of g;
 // otherwise out0 receives the sums of g (the bias gradient). accumulate:
 // out += sums, else out = sums. cols % 4 == 0 and 16-byte aligned rows.
+constexpr int kColStrip = 16;
+constexpr int kRowSlots = 256;  // 16 waves x 16 rows per load
 template <bool LN>
 __global__ __launch_bounds__(1024) void colsum_vec_kernel(const float *__restrict__ g, const float *__restrict__ x,
                                                           const float *__restrict__ means,
@@ -195,15 +199,18 @@ __global__ __launch_bounds__(1024) void colsum_vec_kernel(const float *__restric
                                                           float *__restrict__ out1, int rows, int cols,
                                                           int accumulate) {
   constexpr int kPlanes = LN ? 2 : 1;
-  __shared__ float4 part[kPlanes][64][16];
+  constexpr int kGroups = 64 / kPlanes;            // stage-1 groups per plane and column
+  constexpr int kPerGroup = kRowSlots / kGroups;  // slots per group
+  __shared__ __attribute__((aligned(16))) float part[kPlanes][kRowSlots][kColStrip];
+  __shared__ float grp[kPlanes][kGroups][kColStrip];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int slot = 4 * w + (lane >> 4);
-  const int c4 = lane & 15;
-  const int col = blockIdx.x * 64 + 4 * c4;
+  const int slot = 16 * w + (lane >> 2);
+  const int c4 = lane & 3;
+  const int col = blockIdx.x * kColStrip + 4 * c4;
   float4 a0 = splat4(0.f), a1 = splat4(0.f);
   if (col < cols) {
 #pragma unroll 4
-    for (int r = slot; r < rows; r += 64) {
+    for (int r = slot; r < rows; r += kRowSlots) {
       const float4 gv = *reinterpret_cast<const float4 *>(g + (size_t)r * cols + col);
       if constexpr (LN) {
         const float4 xv = *reinterpret_cast<const float4 *>(x + (size_t)r * cols + col);
@@ -224,17 +231,25 @@ __global__ __launch_bounds__(1024) void colsum_vec_kernel(const float *__restric
       }
     }
   }
-  part[0][slot][c4] = a0;
-  if constexpr (LN) part[kPlanes - 1][slot][c4] = a1;
+  *reinterpret_cast<float4 *>(&part[0][slot][4 * c4]) = a0;
+  if constexpr (LN) *reinterpret_cast<float4 *>(&part[kPlanes - 1][slot][4 * c4]) = a1;
   __syncthreads();
-  if (tid < 64 * kPlanes) {
-    const int plane = tid >> 6, t = tid & 63;
-    const int c = blockIdx.x * 64 + t;
+  {
+    // Stage 1: thread t adds slots kPerGroup*j .. +kPerGroup-1 of column t%16 (j = group).
+    const int c = tid % kColStrip, j = (tid / kColStrip) % kGroups, plane = tid / (kColStrip * kGroups);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kPerGroup; ++k) s += part[plane][kPerGroup * j + k][c];
+    grp[plane][j][c] = s;
+  }
+  __syncthreads();
+  if (tid < kPlanes * kColStrip) {
+    const int plane = tid / kColStrip, t = tid % kColStrip;
+    const int c = blockIdx.x * kColStrip + t;
     float *o = plane ? out1 : out0;
     if (c < cols && o != nullptr) {
-      const float *p = reinterpret_cast<const float *>(&part[plane][0][0]);
       float s = 0.f;
-      for (int k = 0; k < 64; ++k) s += p[k * 64 + t];
+      for (int j = 0; j < kGroups; ++j) s += grp[plane][j][t];
       o[c] = accumulate ? o[c] + s : s;
     }
   }
@@ -412,8 +427,8 @@ template <bool LN>
 void launch_colsum(const float *g, const float *x, const float *means, const float *rstds, float *out0, float *out1,
                    int rows, int cols, int accumulate, bool vec, hipStream_t stream) {
   if (vec)
-    hipLaunchKernelGGL(colsum_vec_kernel<LN>, dim3((cols + 63) / 64), dim3(1024), 0, stream, g, x, means, rstds,
-                       out0, out1, rows, cols, accumulate);
+    hipLaunchKernelGGL(colsum_vec_kernel<LN>, dim3((cols + kColStrip - 1) / kColStrip), dim3(1024), 0, stream, g, x,
+                       means, rstds, out0, out1, rows, cols, accumulate);
   else
     hipLaunchKernelGGL(colsum_generic_kernel<LN>, dim3((cols + 255) / 256), dim3(256), 0, stream, g, x, means,
                        rstds, out0, out1, rows, cols, accumulate);
