@@ -331,6 +331,10 @@ __device__ __forceinline__ void adamw1(float &p, float &m, float &v, float g, fl
 }
 
 // step != nullptr: the bias corrections come from t = *step + 1 on the device.
+// vec: each thread updates float4 groups i and i + 256 of its workgroup's 512
+// (every load of both issued before the arithmetic), the n % 4 tail by the
+// first workgroup; otherwise one value per thread.
+constexpr int kAdamGroups = 2;
 __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float *__restrict__ m,
                                                     float *__restrict__ v, const float *__restrict__ g, size_t n,
                                                     float lr, float b1, float b2, float eps, float wd, float bc1,
@@ -341,25 +345,48 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float
     bc2 = 1.f - powf(b2, t);
   }
   const float decay = 1.f - lr * wd;
-  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
-  size_t done = 0;
-  if (vec) {
-    const size_t n4 = n / 4;
-    for (size_t i = tid; i < n4; i += stride) {
-      float4 pp = reinterpret_cast<float4 *>(p)[i], mm = reinterpret_cast<float4 *>(m)[i];
-      float4 vv = reinterpret_cast<float4 *>(v)[i];
-      const float4 gg = reinterpret_cast<const float4 *>(g)[i];
-      adamw1(pp.x, mm.x, vv.x, gg.x, lr, b1, b2, eps, decay, bc1, bc2);
-      adamw1(pp.y, mm.y, vv.y, gg.y, lr, b1, b2, eps, decay, bc1, bc2);
-      adamw1(pp.z, mm.z, vv.z, gg.z, lr, b1, b2, eps, decay, bc1, bc2);
-      adamw1(pp.w, mm.w, vv.w, gg.w, lr, b1, b2, eps, decay, bc1, bc2);
-      reinterpret_cast<float4 *>(p)[i] = pp;
-      reinterpret_cast<float4 *>(m)[i] = mm;
-      reinterpret_cast<float4 *>(v)[i] = vv;
-    }
-    done = n4 * 4;
+  if (!vec) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) adamw1(p[i], m[i], v[i], g[i], lr, b1, b2, eps, decay, bc1, bc2);
+    return;
   }
-  for (size_t i = done + tid; i < n; i += stride) adamw1(p[i], m[i], v[i], g[i], lr, b1, b2, eps, decay, bc1, bc2);
+  const size_t n4 = n / 4;
+  const size_t base = (size_t)blockIdx.x * (256 * kAdamGroups) + threadIdx.x;
+  float4 pp[kAdamGroups], mm[kAdamGroups], vv[kAdamGroups], gg[kAdamGroups];
+#pragma unroll
+  for (int k = 0; k < kAdamGroups; ++k) {
+    const size_t i = base + 256 * k;
+    if (i < n4) {
+      pp[k] = reinterpret_cast<const float4 *>(p)[i];
+      mm[k] = reinterpret_cast<const float4 *>(m)[i];
+      vv[k] = reinterpret_cast<const float4 *>(v)[i];
+      gg[k] = reinterpret_cast<const float4 *>(g)[i];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kAdamGroups; ++k) {
+    const size_t i = base + 256 * k;
+    if (i < n4) {
+      adamw1(pp[k].x, mm[k].x, vv[k].x, gg[k].x, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp[k].y, mm[k].y, vv[k].y, gg[k].y, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp[k].z, mm[k].z, vv[k].z, gg[k].z, lr, b1, b2, eps, decay, bc1, bc2);
+      adamw1(pp[k].w, mm[k].w, vv[k].w, gg[k].w, lr, b1, b2, eps, decay, bc1, bc2);
+      reinterpret_cast<float4 *>(p)[i] = pp[k];
+      reinterpret_cast<float4 *>(m)[i] = mm[k];
+      reinterpret_cast<float4 *>(v)[i] = vv[k];
+    }
+  }
+  if (blockIdx.x == 0) {
+    const size_t i = n4 * 4 + threadIdx.x;
+    if (i < n) adamw1(p[i], m[i], v[i], g[i], lr, b1, b2, eps, decay, bc1, bc2);
+  }
+}
+
+// Workgroups of the AdamW kernel over n values.
+unsigned adamw_blocks(size_t n, int vec) {
+  const size_t per = vec ? (size_t)256 * kAdamGroups * 4 : 256;
+  const size_t b = (n + per - 1) / per;
+  return (unsigned)(b < 1 ? 1 : b);
 }
 
 __global__ void step_advance_kernel(float *step) {
@@ -528,7 +555,7 @@ extern "C" int dfgpt2_adamw_update(float *parameter, float *first_moment, float 
     return st;
   const int vec = (al(parameter, 16) && al(first_moment, 16) && al(second_moment, 16) && al(gradient, 16)) ? 1 : 0;
   if (n > 0) {
-    hipLaunchKernelGGL(adamw_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, stream, parameter, first_moment,
+    hipLaunchKernelGGL(adamw_kernel, dim3(adamw_blocks(n, vec)), dim3(256), 0, stream, parameter, first_moment,
                        second_moment, gradient, n, lr, beta1, beta2, eps, weight_decay, 1.f, 1.f, step, vec);
     if (int st = launched(fn); st != DFATTN_OK) return st;
   }
@@ -569,7 +596,7 @@ extern "C" void launch_adamw_update(float *parameter, float *first_moment, float
   int st = check_ptrs(fn, {parameter, first_moment, second_moment, gradient}, {});
   if (st == DFATTN_OK && n > 0) {
     const int vec = (al(parameter, 16) && al(first_moment, 16) && al(second_moment, 16) && al(gradient, 16)) ? 1 : 0;
-    hipLaunchKernelGGL(adamw_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, nullptr, parameter, first_moment,
+    hipLaunchKernelGGL(adamw_kernel, dim3(adamw_blocks(n, vec)), dim3(256), 0, nullptr, parameter, first_moment,
                        second_moment, gradient, (size_t)n, lr, beta1, beta2, eps, weight_decay, bias_correction1,
                        bias_correction2, nullptr, vec);
     st = launched(fn);
