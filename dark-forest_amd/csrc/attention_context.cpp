@@ -7,12 +7,14 @@
 //  * Every buffer the context needs is allocated at construction (logsumexp
 //    [H, S] and the backward workspace, O(H*S) and O(H*S*D)); the reference allocates
 //    an H*2*S*S probability scratch on the first backward (lib.rs:2019-2027).
-//  * backward_device_into reuses the O and logsumexp that forward_device_into
-//    wrote when it is called with the same q, k, v pointers (the reference's
-//    static engine keeps a layer's Q, K, V and O untouched between the two,
-//    static_gpt2.rs:1329-1336, 1500-1510). With other pointers it first
-//    recomputes them into context-owned buffers, so results never depend on
-//    the order of calls.
+//  * backward_device_into recomputes the forward from the current contents of
+//    q, k, v (as the reference's does, lib.rs:2240-2293) into context-owned
+//    buffers. A caller that keeps a layer's Q, K, V and O untouched between
+//    the two calls, as the reference's static engine does
+//    (static_gpt2.rs:1329-1336, 1500-1510), may opt in to reusing the last
+//    forward_device_into's O, logsumexp and fp16 operand copies instead
+//    (dfattn_context_set_reuse_forward); reuse then also needs the same q, k,
+//    v pointers, scale and causal flag.
 //  * Errors are status codes (dfattn_status) instead of anyhow::Result.
 #include <hip/hip_runtime.h>
 
@@ -36,6 +38,9 @@ struct dfattn_context {
   const float *last_out = nullptr;
   float last_scale = 0.f;
   uint32_t last_causal = 0;
+  // Opt-in: the backward may reuse the last forward (caller guarantees that
+  // q, k, v and that forward's out are unchanged and still allocated).
+  bool reuse_forward = false;
   // Context-owned O, allocated on first need (a backward without a matching
   // forward, or the host-slice forward).
   float *own_out = nullptr;
@@ -96,7 +101,7 @@ int run_backward(dfattn_context *c, const float *q, const float *k, const float 
                  const float *d_out, float scale, uint32_t causal, float *d_q, float *d_k,
                  float *d_v, void *stream) {
   const float *o = c->last_out;
-  if (!(q == c->last_q && k == c->last_k && v == c->last_v && o != nullptr &&
+  if (!(c->reuse_forward && q == c->last_q && k == c->last_k && v == c->last_v && o != nullptr &&
         scale == c->last_scale && causal == c->last_causal)) {
     int st = ensure(&c->own_out, c->elems);
     if (st != DFATTN_OK) return st;
@@ -172,6 +177,13 @@ int dfattn_context_dims(const dfattn_context *c, uint32_t *n_heads, uint32_t *se
 }
 
 const float *dfattn_context_lse(const dfattn_context *c) { return c ? c->lse : nullptr; }
+
+int dfattn_context_set_reuse_forward(dfattn_context *c, uint32_t enable) {
+  if (c == nullptr) return fail(DFATTN_ERR_NULL_POINTER, "null attention context");
+  std::lock_guard<std::mutex> lock(c->mu);
+  c->reuse_forward = enable != 0;
+  return DFATTN_OK;
+}
 
 int dfattn_context_forward_device_into(dfattn_context *c, const float *q, const float *k,
                                        const float *v, float scale, uint32_t causal, float *out,

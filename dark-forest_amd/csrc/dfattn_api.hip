@@ -291,15 +291,19 @@ void launch_fused_mha_backward(const float *q, const float *k, const float *v,
 }
 
 void darkforest_sync(void) {
+  // A recorded launcher error aborts before any HIP call: nothing was
+  // launched for it, so there is no device work to wait for first.
+  {
+    std::lock_guard<std::mutex> lock(g_err_mu);
+    if (g_pending != DFATTN_OK) {
+      fprintf(stderr, "[darkforest] attention launch error before sync boundary: %s\n",
+              g_pending_msg.c_str());
+      abort();
+    }
+  }
   hipError_t err = hipDeviceSynchronize();
   if (err != hipSuccess) {
     fprintf(stderr, "[darkforest] HIP kernel error at sync boundary: %s\n", hipGetErrorString(err));
-    abort();
-  }
-  std::lock_guard<std::mutex> lock(g_err_mu);
-  if (g_pending != DFATTN_OK) {
-    fprintf(stderr, "[darkforest] attention launch error before sync boundary: %s\n",
-            g_pending_msg.c_str());
     abort();
   }
 }

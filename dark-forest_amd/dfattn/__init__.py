@@ -72,6 +72,7 @@ SYMBOLS = {
     "dfattn_context_destroy": (None, [_P]),
     "dfattn_context_dims": (ctypes.c_int, [_P] + [ctypes.POINTER(_U32)] * 4),
     "dfattn_context_lse": (_P, [_P]),
+    "dfattn_context_set_reuse_forward": (ctypes.c_int, [_P, _U32]),
     "dfattn_context_forward_device_into": (ctypes.c_int, [_P] * 4 + [_F, _U32, _P, ctypes.c_size_t, _P]),
     "dfattn_context_backward_device_into": (ctypes.c_int,
                                             [_P] * 5 + [_F, _U32, _P, _P, _P, ctypes.c_size_t, _P]),
@@ -390,12 +391,26 @@ class AttentionContext:
     seq_len * d_head floats and run one head, as the reference's do.
     """
 
-    def __init__(self, n_heads, seq_len, d_head):
+    def __init__(self, n_heads, seq_len, d_head, reuse_forward=False):
         handle = ctypes.c_void_p()
         _check(lib().dfattn_context_create(n_heads, seq_len, d_head, ctypes.byref(handle)))
         self._h = handle
         self.n_heads, self.seq_len, self.d_head = n_heads, seq_len, d_head
         self.d_model = n_heads * d_head
+        self._last = None  # q, k, v, out of the last device forward (kept alive while reuse is on)
+        self.reuse_forward = False
+        if reuse_forward:
+            self.set_reuse_forward(True)
+
+    def set_reuse_forward(self, enable):
+        """dfattn_context_set_reuse_forward: let backward_device_into reuse the last
+        forward_device_into on the same q, k, v (the caller promises not to modify q, k, v or that
+        forward's out in between). This wrapper keeps those four tensors referenced, so they
+        cannot be freed and reused by torch's allocator while the context may still read them."""
+        _check(lib().dfattn_context_set_reuse_forward(self._h, int(bool(enable))))
+        self.reuse_forward = bool(enable)
+        if not enable:
+            self._last = None
 
     def close(self):
         if getattr(self, "_h", None):
@@ -418,6 +433,8 @@ class AttentionContext:
         _check(lib().dfattn_context_forward_device_into(
             self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), scale, int(bool(causal)), _dev_ptr(out),
             self._elems(out) & ((1 << 64) - 1), _stream_ptr(stream)))
+        if self.reuse_forward:
+            self._last = (q, k, v, out)
 
     def forward_device(self, q, k, v, scale, causal, stream=None):
         """lib.rs:2029: allocate O and run forward_device_into."""

@@ -287,6 +287,15 @@ int dfattn_context_dims(const dfattn_context *ctx, uint32_t *n_heads, uint32_t *
  * forward (device pointer; NULL for a NULL context).                        */
 const float *dfattn_context_lse(const dfattn_context *ctx);
 
+/* Opt-in forward reuse for the backward (no reference counterpart; the
+ * reference always recomputes). enable != 0 promises that between a
+ * forward_device_into and the backward_device_into on the same q, k, v,
+ * neither q, k, v nor that forward's `out` is modified or freed — the
+ * reference's static engine keeps them in its arena untouched
+ * (static_gpt2.rs:1329-1336, 1500-1510). Breaking the promise gives stale
+ * gradients (or reads freed memory as O); it is not detected.              */
+int dfattn_context_set_reuse_forward(dfattn_context *ctx, uint32_t enable);
+
 /* lib.rs:2042 forward_device_into: O [seq_len, d_model] from device Q, K, V;
  * out_elems must equal seq_len * d_model ("attention output shape
  * mismatch"). Also writes the context's logsumexp and remembers q, k, v and
@@ -296,10 +305,11 @@ int dfattn_context_forward_device_into(dfattn_context *ctx, const float *q, cons
                                        float *out, size_t out_elems, void *stream);
 
 /* lib.rs:2240 backward_device_into: dQ, dK, dV (each seq_len * d_model =
- * grad_elems). Uses the O and logsumexp of the last forward_device_into on
- * the same q, k, v, scale and causal (the caller keeps that O unmodified in
- * between, as the reference engine does, static_gpt2.rs:1329-1336,
- * 1500-1510); otherwise recomputes them first.                              */
+ * grad_elems), computed from the current contents of q, k, v and d_out: by
+ * default the forward is recomputed first, as the reference does. With
+ * reuse enabled (dfattn_context_set_reuse_forward) and the same q, k, v
+ * pointers, scale and causal flag as the last forward_device_into, the O,
+ * logsumexp and fp16 operand copies of that forward are reused instead.    */
 int dfattn_context_backward_device_into(dfattn_context *ctx, const float *q, const float *k,
                                         const float *v, const float *d_out, float scale,
                                         uint32_t causal, float *d_q, float *d_k, float *d_v,

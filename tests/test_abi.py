@@ -114,6 +114,24 @@ def test_legacy_launcher_records_error_instead_of_launching():
     lib.dfattn_clear_error()
 
 
+def test_sync_aborts_for_a_recorded_launcher_error_before_any_hip_call():
+    """darkforest_sync aborts with the reference's "[darkforest] ..." message for an argument error
+    of a void launcher (matmul.cu:21-28). The launcher records the error on the host without
+    launching, and darkforest_sync checks it before touching the device, so the child process that
+    aborts here never initialises HIP (its GPUs are hidden as well)."""
+    import subprocess
+    import sys
+
+    pkg = os.path.join(ROOT, "dark-forest_amd")
+    launcher = ("import sys; sys.path.insert(0, %r); import ctypes, dfattn; lib = dfattn.lib(); "
+                "f = ctypes.c_void_p(0x10000); lib.launch_fused_mha_forward(f, f, f, f, 12, 128, 129, 0.1, 1); "
+                "lib.darkforest_sync(); print('survived')") % pkg
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1", ROCR_VISIBLE_DEVICES="-1")
+    out = subprocess.run([sys.executable, "-c", launcher], capture_output=True, text=True, timeout=120, env=env)
+    assert out.returncode != 0 and "survived" not in out.stdout
+    assert "[darkforest] attention launch error" in out.stderr, out.stderr
+
+
 def test_product_path_never_touches_the_oracle():
     """Only tests/, smoke() and bench.py's cpu_baseline may use oracle/."""
     pkg = os.path.join(ROOT, "dark-forest_amd")

@@ -135,9 +135,10 @@ def test_autograd_function_matches_float64_torch(device):
         close(name, t.grad.cpu().numpy(), r.grad.transpose(0, 1).reshape(s, h * d).numpy())
 
 
-def test_sync_aborts_only_for_launcher_errors(device):
-    """darkforest_sync aborts for an argument error of a void launcher (the reference's behaviour,
-    matmul.cu:21-28) but not for an error a status-returning entry point already returned."""
+def test_sync_survives_errors_already_returned(device):
+    """darkforest_sync does not abort for an error a status-returning entry point already returned
+    (it synchronises the device and returns). Its aborting branch, for an argument error of a void
+    launcher, is host-only logic and is tested on the CPU (test_abi.py)."""
     import subprocess
     import sys
 
@@ -149,9 +150,57 @@ def test_sync_aborts_only_for_launcher_errors(device):
                 "lib.darkforest_sync(); print('survived')") % pkg
     out = subprocess.run([sys.executable, "-c", returned], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and "survived" in out.stdout, out.stderr
-    launcher = ("import sys; sys.path.insert(0, %r); import ctypes, dfattn; lib = dfattn.lib(); "
-                "f = ctypes.c_void_p(0x10000); lib.launch_fused_mha_forward(f, f, f, f, 12, 128, 129, 0.1, 1); "
-                "lib.darkforest_sync(); print('survived')") % pkg
-    out = subprocess.run([sys.executable, "-c", launcher], capture_output=True, text=True, timeout=120)
-    assert out.returncode != 0 and "survived" not in out.stdout
-    assert "[darkforest] attention launch error" in out.stderr
+
+
+def test_context_backward_reads_current_q_after_in_place_change(device):
+    """By default backward_device_into differentiates the current contents of q, k, v (the
+    reference recomputes, lib.rs:2240-2293): q changed in place after the forward, and the
+    forward's O dropped, still give the oracle's gradients of the new q."""
+    import gc
+
+    import torch
+
+    h, s, d = 12, 192, 64
+    say("context: q changed in place between forward and backward")
+    x = O.seeded_inputs(s, h, d, 11500)
+    q, k, v, g = (dev(x[n], device) for n in ("q", "k", "v", "do"))
+    ctx = dfattn.AttentionContext(h, s, d)
+    out = ctx.forward_device(q, k, v, 0.125, True)
+    del out
+    gc.collect()
+    torch.cuda.empty_cache()
+    q.mul_(0.5).add_(0.25)
+    junk = torch.full((s, h * d), float("nan"), device=device)  # may take the freed O's block
+    dq, dk, dv = ctx.backward_device(q, k, v, g, 0.125, True)
+    torch.cuda.synchronize()
+    q_new = (x["q"] * np.float32(0.5) + np.float32(0.25)).astype(np.float32)
+    want = O.backward(q_new, x["k"], x["v"], x["do"], h, 0.125, True, threads=8)
+    for name, got, w in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        close(name, got.cpu().numpy(), w)
+    del junk
+    ctx.close()
+
+
+def test_context_reuse_forward_matches_recompute(device):
+    """With forward reuse on (the engine's contract: q, k, v and O untouched in between) the backward
+    gives the recomputing backward's gradients bit for bit, and the wrapper holds the forward's
+    tensors while the context may read them."""
+    import torch
+
+    h, s, d = 12, 320, 64
+    say("context: opt-in forward reuse")
+    x = O.seeded_inputs(s, h, d, 11600)
+    q, k, v, g = (dev(x[n], device) for n in ("q", "k", "v", "do"))
+    plain = dfattn.AttentionContext(h, s, d)
+    ref = plain.backward_device(q, k, v, g, 0.125, True)
+    reuse = dfattn.AttentionContext(h, s, d, reuse_forward=True)
+    out = reuse.forward_device(q, k, v, 0.125, True)
+    assert reuse._last is not None and reuse._last[3] is out
+    got = reuse.backward_device(q, k, v, g, 0.125, True)
+    torch.cuda.synchronize()
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    reuse.set_reuse_forward(False)
+    assert reuse._last is None
+    plain.close()
+    reuse.close()

@@ -24,9 +24,12 @@ def say(msg):
     print(f"[gpu-gpt2] {msg}", flush=True)
 
 
-def test_loss_parity_against_sdpa_twin(device):
-    say("loss parity tiny config")
-    cfg = dict(vocab_size=500, d_model=128, n_heads=4, n_layers=2, d_ff=512, seq_len=64, lr=1e-3, seed=5)
+@pytest.mark.parametrize("n_heads", [4, 2])
+def test_loss_parity_against_sdpa_twin(device, n_heads):
+    """n_heads 4 gives d_head 32 (the exact fp32 kernels); n_heads 2 gives d_head 64, the fp16-operand
+    MFMA forward and backward GPT-2 small uses, held to the same bar across optimizer steps."""
+    say(f"loss parity tiny config, {n_heads} heads (d_head {128 // n_heads})")
+    cfg = dict(vocab_size=500, d_model=128, n_heads=n_heads, n_layers=2, d_ff=512, seq_len=64, lr=1e-3, seed=5)
     ours = StaticGPT2(**cfg, attention="dfattn")
     twin = StaticGPT2(**cfg, attention="sdpa")
     twin.load_state(ours)

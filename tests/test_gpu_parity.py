@@ -105,6 +105,34 @@ def test_c2_fwd_bwd_s4096(device):
     compare("C2", run_fwd_bwd(x, 12, 0.125, True, device), oracle_fwd_bwd(x, 12, 0.125, True))
 
 
+def run_training_pair(x, n_heads, scale, causal, device):
+    """bench.py's timed step exactly: dfattn_fwd_train, dfattn_bwd_preprocess(DFATTN_BWD_QKV_SAVED),
+    dfattn_bwd_main, with one workspace (filled with NaN first, so nothing stale is read)."""
+    import torch
+
+    q, k, v, g = (to_dev(x[n], device) for n in ("q", "k", "v", "do"))
+    seq_len, dm = q.shape
+    ws = torch.full((dfattn.bwd_workspace_bytes(n_heads, seq_len, dm // n_heads) // 4,), float("nan"),
+                    device=device)
+    o, lse = dfattn.forward_train(q, k, v, n_heads, ws, scale, causal)
+    grads = [torch.empty_like(q) for _ in range(3)]
+    dfattn.backward_preprocess(q, k, v, o, g, lse, ws, n_heads, scale, flags=dfattn.BWD_QKV_SAVED)
+    dfattn.backward_main(q, k, v, o, g, lse, *grads, ws, n_heads, scale, causal)
+    torch.cuda.synchronize()
+    return {"o": host(o), "lse": host(lse), "dq": host(grads[0]), "dk": host(grads[1]), "dv": host(grads[2])}
+
+
+@pytest.mark.parametrize("seq_len,seed", [(1024, 2000), (1024, 2500), (4096, 3000), (4096, 3500)])
+def test_timed_training_pair_matches_oracle(device, seq_len, seed):
+    """The sequence bench.py times (C1 and C2 shapes; seed 3000 is bench.py's own input) against the
+    oracle at the north star's bar, on two seeds each. Prints every tensor's max-abs / rel-L2 so the
+    margin to the 2e-3 bar is on record."""
+    say(f"timed training pair H=12 S={seq_len} seed {seed}")
+    x = O.seeded_inputs(seq_len, 12, 64, seed)
+    compare(f"pair S={seq_len} seed={seed}", run_training_pair(x, 12, 0.125, True, device),
+            oracle_fwd_bwd(x, 12, 0.125, True))
+
+
 # ---------------------------------------------------------------- ragged shapes and modes
 @pytest.mark.parametrize("seq_len", [1, 2, 31, 33, 63, 64, 65, 127, 129, 200, 1000])
 @pytest.mark.parametrize("causal", [True, False])
@@ -272,8 +300,8 @@ def test_c3_long_context_forward_rows_and_memory(device):
     assert np.all(np.abs(o_all) <= np.abs(x["v"]).max() + 1e-3)
 
 
-@pytest.mark.parametrize("seq_len,seed", [(4096, 3100), (16384, 3200)])
-def test_backward_invariants(device, seq_len, seed):
+@pytest.mark.parametrize("seq_len,n_heads,seed", [(4096, 12, 3100), (16384, 12, 3200), (65536, 2, 3300)])
+def test_backward_invariants(device, seq_len, n_heads, seed):
     """Rows of P sum to one, so per head and column: sum_j dV_j = sum_i dO_i and sum_j dK_j = 0.
 
     The identities are exact for any inputs; what the GPU leaves over is the fp16
@@ -282,10 +310,12 @@ def test_backward_invariants(device, seq_len, seed):
     deviations). A lost or doubled key block, a wrong head offset or a dropped
     Delta term leaves residuals of order max|column| * S, far above it. S=16384
     is past what the CPU oracle does in seconds; only the identities check it.
+    S=65536 has more key and query tiles than the backward's host-built dispatch
+    table holds, so its workgroups find their items with the in-kernel search.
     """
-    say(f"invariants S={seq_len}")
-    x = O.seeded_inputs(seq_len, 12, 64, seed)
-    got = run_fwd_bwd(x, 12, 0.125, True, device)
+    say(f"invariants S={seq_len} H={n_heads}")
+    x = O.seeded_inputs(seq_len, n_heads, 64, seed)
+    got = run_fwd_bwd(x, n_heads, 0.125, True, device)
     u = 2.0 ** -11
 
     def bar(col):
