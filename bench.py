@@ -15,11 +15,15 @@ causal forward = 2*H*S^2*D, backward = 2.5x forward, so one step = 7*H*S^2*D
 
 Prints ONE JSON line. `roofline` is for the dominant kernel (the one with the
 largest average duration, timed live with HIP events on the stream the
-library launches on, in a second pass after the timed one; `frac_at_sclk`
-also divides by the peak at the shader clock rocm-smi reports while the step
-runs); `cpu_baseline` times the CPU oracle (a restatement of the reference's
-fp32 CPU attention) on a bounded sample of the same workload on one thread,
-`cpu_baseline_threads` on every head in parallel.
+library launches on, around `steps` back-to-back launches of each phase in a
+second pass after the timed one; `frac_at_sclk` also divides by the peak at
+the shader clock rocm-smi reports while the step runs; `traffic` comes from
+the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary only when that summary
+was taken on this build's kernel sources, else null); `cpu_baseline` times
+the CPU oracle (a restatement of the reference's fp32 CPU attention) on a
+bounded sample of the same workload on one thread, `cpu_baseline_threads` on
+every head in parallel, `cpu_baseline_configs` every BASELINE attention
+config (C3 extrapolated from sampled rows).
 """
 from __future__ import annotations
 
@@ -53,8 +57,16 @@ def seeded(seq_len, n_heads, d_head, seed):
             for i in range(4)]
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
+    except OSError:
+        return ""
+
+
 def cpu_baseline(heads: int):
-    """The CPU oracle (oracle/attention_oracle.c), 1 thread, on `heads` of the 12 heads."""
+    """The CPU oracle (oracle/attention_oracle.c), 1 thread, on `heads` of the 12 heads of C2."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
@@ -69,7 +81,7 @@ def cpu_baseline(heads: int):
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"heads 0..{heads - 1} of {H} at S={S}, D={D}: causal fwd+bwd, fp32, 1 thread "
                       f"({dt:.1f} s; {flops / 1e9:.2f} GFLOP algorithmic)",
-            "seconds": round(dt, 3)}
+            "seconds": round(dt, 3), "heads": heads}
 
 
 def cpu_baseline_threads():
@@ -83,16 +95,68 @@ def cpu_baseline_threads():
     O.mha_forward(q, k, v, H, SCALE, True, threads=threads)
     O.backward(q, k, v, g, H, SCALE, True, threads=threads)
     dt = time.perf_counter() - t0
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
-    except OSError:
-        pass
     return {"value": FLOP_STEP / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"all {H} heads at S={S}, D={D}: causal fwd+bwd, fp32, {threads} threads over heads "
                       f"({dt:.1f} s)", "seconds": round(dt, 3), "cpus_available": len(os.sched_getaffinity(0)),
-            "cpu_model": model}
+            "cpu_model": _cpu_model()}
+
+
+def cpu_baseline_configs(c2_one_thread=None):
+    """The CPU oracle, 1 thread, on every BASELINE attention config (C0-C3), in ms and GFLOP/s.
+
+    C0 (fwd, S=128) and C1 (fwd+bwd, S=1024) run in full, median of 3. C2 (fwd+bwd, S=4096) is the
+    `cpu_baseline` sample (6 of 12 heads) scaled to 12 heads. C3 (fwd, S=131072) is extrapolated:
+    the oracle's forward on a stratified sample of query rows (every head), timed, scaled by the
+    exact number of causal (query, key) pairs S(S+1)/2 over the sample's pairs.
+    """
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    rows = []
+
+    def median3(fn):
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[1]
+
+    x = O.seeded_inputs(128, H, D, 1000, with_grad=False)
+    dt = median3(lambda: O.mha_forward(x["q"], x["k"], x["v"], H, SCALE, True, threads=1))
+    fl = 2.0 * H * 128 * 128 * D
+    rows.append({"config": "C0 fwd S=128", "ms": round(dt * 1e3, 3), "gflops": round(fl / dt / 1e9, 3),
+                 "how": "full, median of 3"})
+    x = O.seeded_inputs(1024, H, D, 2000)
+
+    def c1():
+        O.mha_forward(x["q"], x["k"], x["v"], H, SCALE, True, threads=1)
+        O.backward(x["q"], x["k"], x["v"], x["do"], H, SCALE, True, threads=1)
+
+    dt = median3(c1)
+    fl = 7.0 * H * 1024 * 1024 * D
+    rows.append({"config": "C1 fwd+bwd S=1024", "ms": round(dt * 1e3, 1), "gflops": round(fl / dt / 1e9, 3),
+                 "how": "full, median of 3"})
+    if c2_one_thread is not None:
+        dt = c2_one_thread["seconds"] * H / c2_one_thread["heads"]
+        rows.append({"config": "C2 fwd+bwd S=4096", "ms": round(dt * 1e3, 1), "gflops": round(FLOP_STEP / dt / 1e9, 3),
+                     "how": f"{c2_one_thread['heads']} of {H} heads timed, scaled to {H}"})
+    s3 = 131072
+    x = O.seeded_inputs(s3, H, D, 9000, std=0.5, with_grad=False)
+    sample = np.unique(np.concatenate([np.linspace(0, s3 - 1, 5).astype(np.int64),
+                                       np.random.default_rng(3).integers(0, s3, 3)]))
+    t0 = time.perf_counter()
+    O.mha_forward_rows(x["q"], x["k"], x["v"], sample, H, SCALE, True, threads=1)
+    dt = time.perf_counter() - t0
+    pairs_sample = float(np.sum(sample + 1))
+    pairs_total = s3 * (s3 + 1) / 2.0
+    dt_full = dt * pairs_total / pairs_sample
+    fl = 2.0 * H * s3 * s3 * D
+    rows.append({"config": "C3 fwd S=131072", "ms": round(dt_full * 1e3, 0), "gflops": round(fl / dt_full / 1e9, 3),
+                 "how": f"extrapolated: {sample.size} stratified query rows x {H} heads timed ({dt:.2f} s), "
+                        f"scaled by S(S+1)/2 / sampled causal pairs"})
+    return {"cores": 1, "kind": "port", "nproc": len(os.sched_getaffinity(0)), "cpu_model": _cpu_model(),
+            "rows": rows}
 
 
 def sample_sclk(step, seconds=1.5):
@@ -133,6 +197,21 @@ def sample_sclk(step, seconds=1.5):
 
 
 TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_c2_hbm_traffic.md")
+CSRC = os.path.join(ROOT, "dark-forest_amd", "csrc")
+
+
+def kernel_source_hash():
+    """First 12 hex digits of a SHA-256 over the library's kernel sources (csrc/*.hip, *.h, *.cpp),
+    which stamps a counter profile with the build it describes."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            h.update(name.encode())
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:12]
 KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_convert_kernel", "bwd_main_kernel")
 
 
@@ -154,14 +233,19 @@ def short_kernel_name(name):
 
 
 def load_traffic():
-    """HBM bytes per launch of each kernel, from the committed rocprofv3 --pmc summary.
+    """HBM bytes per launch of each kernel, from the committed rocprofv3 --pmc summary, or {} when
+    that summary was not taken on the kernel sources of this build.
 
-    The summary's table rows read `| kernel | fetch KiB | write KiB | HBM bytes per launch |`.
+    The summary carries a line `Kernel sources: <kernel_source_hash()>` and table rows
+    `| kernel | fetch KiB | write KiB | HBM bytes per launch |`.
     """
     if not os.path.exists(TRAFFIC_MD):
         return {}
+    text = open(TRAFFIC_MD).read()
+    if f"Kernel sources: {kernel_source_hash()}" not in text:
+        return {}
     out = {}
-    for line in open(TRAFFIC_MD):
+    for line in text.splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) == 4 and cells[0] in KERNELS:
             out[cells[0]] = int(float(cells[3]))
@@ -189,7 +273,8 @@ def summarize_pmc(fetch_csv, write_csv, copy_mib):
     known_kib = copy_mib * 1024.0
     f_fac = known_kib / fetch["copyBuffer"]
     w_fac = known_kib / write["copyBuffer"]
-    lines = [f"Copy calibration ({copy_mib} MiB read + {copy_mib} MiB written): FETCH_SIZE reads "
+    lines = [f"Kernel sources: {kernel_source_hash()}", "",
+             f"Copy calibration ({copy_mib} MiB read + {copy_mib} MiB written): FETCH_SIZE reads "
              f"{fetch['copyBuffer']:.0f} KiB (factor {f_fac:.3f}), WRITE_SIZE reads {write['copyBuffer']:.0f} KiB "
              f"(factor {w_fac:.3f}).", "",
              "| kernel | fetch KiB | write KiB | HBM bytes per launch |", "|---|---|---|---|"]
@@ -409,7 +494,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-heads", type=int, default=6, help="heads in the CPU baseline sample (0 = skip)")
-    ap.add_argument("--gpt2-steps", type=int, default=10,
+    ap.add_argument("--gpt2-steps", type=int, default=20,
                     help="timed GPT-2 small training steps at S=1024 (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, run 5 plain device copies of MIB MiB each (the known-size kernel "
@@ -464,18 +549,10 @@ def main():
     ws = torch.empty(dfattn.bwd_workspace_bytes(H, S, D) // 4, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream()
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
+    def step():
         dfattn.forward_train(q, k, v, H, ws, SCALE, True, out=o, lse=lse)
-        if ev is not None:
-            ev[1].record(stream)
         dfattn.backward_preprocess(q, k, v, o, g, lse, ws, H, SCALE, flags=dfattn.BWD_QKV_SAVED)
-        if ev is not None:
-            ev[2].record(stream)
         dfattn.backward_main(q, k, v, o, g, lse, dq, dk, dv, ws, H, SCALE, True)
-        if ev is not None:
-            ev[3].record(stream)
 
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
@@ -491,17 +568,30 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
-    # A second pass with HIP events on the library's stream around every launch gives the
-    # per-kernel durations (the events add their own packets, so they stay out of the timed region).
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        step(events[i])
-    torch.cuda.synchronize()
+    # Per-kernel durations, outside the timed region: each phase launched `steps` times back to
+    # back between two HIP events on the library's stream (the launches are idempotent on these
+    # inputs), so the events' own packets do not sit between the kernels; then whole steps between
+    # events for the step's spread.
+    def phase_ms(fn):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(stream)
+        for _ in range(args.steps):
+            fn()
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / args.steps
 
-    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
-    pre_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
-    main_ms = float(np.mean([e[2].elapsed_time(e[3]) for e in events]))
-    step_ev_ms = sorted(e[0].elapsed_time(e[3]) for e in events)
+    fwd_ms = phase_ms(lambda: dfattn.forward_train(q, k, v, H, ws, SCALE, True, out=o, lse=lse))
+    pre_ms = phase_ms(lambda: dfattn.backward_preprocess(q, k, v, o, g, lse, ws, H, SCALE,
+                                                         flags=dfattn.BWD_QKV_SAVED))
+    main_ms = phase_ms(lambda: dfattn.backward_main(q, k, v, o, g, lse, dq, dk, dv, ws, H, SCALE, True))
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        events[i][0].record(stream)
+        step()
+        events[i][1].record(stream)
+    torch.cuda.synchronize()
+    step_ev_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
     log(f"fwd {fwd_ms:.4f} ms, bwd preprocess {pre_ms:.4f} ms, bwd main {main_ms:.4f} ms, wall/step {ms_per_step:.4f} ms")
 
     kernels = {
@@ -594,6 +684,8 @@ def main():
         result["cpu_baseline"] = cpu_baseline(args.cpu_heads)
         log("cpu baseline, all heads, parallel over heads")
         result["cpu_baseline_threads"] = cpu_baseline_threads()
+        log("cpu baseline, every BASELINE attention config (C3 extrapolated from sampled rows)")
+        result["cpu_baseline_configs"] = cpu_baseline_configs(result["cpu_baseline"])
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -104,6 +104,14 @@ def lib():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise DfattnNotBuilt(f"{LIB_PATH} not found; build it with __graft_entry__.build()")
+    # The library and torch must share one HIP runtime: the wrappers pass torch's streams and device
+    # pointers to it. torch bundles its own libamdhip64 under the same soname, so loading torch first
+    # makes the dynamic linker bind the library to that copy; loaded the other way round the process
+    # would hold two runtimes, and the one the library uses may not see the GPU.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     handle = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SYMBOLS.items():
         fn = getattr(handle, name)
