@@ -419,6 +419,74 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v, const float 
   return record_hip(err, "attention backward launch");
 }
 
+}  // extern "C"
+
+// ---- backward without allocation -------------------------------------------
+// The backward's workspace in a static device array, for callers that cannot
+// allocate (code under graph capture, serving loops, harnesses that forbid
+// hipMalloc). Each device holds its own copy of the array from the library's
+// load until the process ends; in host code `scratch` only names the symbol,
+// its device address comes from hipGetSymbolAddress, once per device.
+namespace {
+static __device__ __align__(256) unsigned char scratch[DFATTN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the current device (looked up on the first
+// call on each device, with that device current).
+int scratch_on_current_device(const char *fn, void **out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return record_hip(err, fn);
+  if (dev < 0 || dev >= kMaxDevices)
+    return record_error(DFATTN_ERR_HIP, std::string(fn) + ": device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return record_hip(err, fn);
+    if (p == nullptr) return record_error(DFATTN_ERR_HIP, std::string(fn) + ": scratch symbol has no address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DFATTN_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int dfattn_bwd_noalloc(const float *q, const float *k, const float *v, const float *o, const float *d_o,
+                       const float *lse, float *d_q, float *d_k, float *d_v, uint32_t n_heads,
+                       uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal, void *stream) {
+  const char *fn = "dfattn_bwd_noalloc";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse, d_q, d_k, d_v});
+  if (st != DFATTN_OK) return st;
+  const size_t need = dfattn_bwd_workspace_bytes(n_heads, seq_len, d_head);
+  if (need > (size_t)DFATTN_NOALLOC_SCRATCH_BYTES)
+    return record_error(DFATTN_ERR_WORKSPACE,
+                        std::string(fn) + ": this shape needs " + std::to_string(need) +
+                            " bytes of backward workspace, more than the static scratch holds (" +
+                            std::to_string((size_t)DFATTN_NOALLOC_SCRATCH_BYTES) + "); use dfattn_bwd");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err;
+  if (fast_path(d_head, {q, k, v, o, d_o, lse, d_q, d_k, d_v})) {
+    void *ws = nullptr;
+    st = scratch_on_current_device(fn, &ws);
+    if (st != DFATTN_OK) return st;
+    // Preprocess overwrites every workspace value the main kernel reads, so
+    // nothing has to be cleared between calls.
+    err = dfattn::launch_bwd_d64(q, k, v, o, d_o, lse, d_q, d_k, d_v, ws, (int)n_heads, (int)seq_len, scale,
+                                 causal != 0, s);
+  } else {
+    err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len, (int)d_head,
+                                     scale, causal != 0, s);
+  }
+  return record_hip(err, "attention backward launch");
+}
+
 // ---- decode ----------------------------------------------------------------
 
 void launch_fused_mha_decode_kv(const float *q, const float *k_cache, const float *v_cache, float *out,

@@ -52,6 +52,7 @@ SYMBOLS = {
     "dfattn_fwd_train": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_bwd_noalloc": (ctypes.c_int, [_P] * 9 + [_U32, _U32, _U32, _F, _U32, _P]),
     "launch_fused_mha_decode_kv": (None, [_P] * 4 + [_U32, _U32, _U32, _F]),
     "launch_fused_mha_decode_kv_splitk": (None, [_P] * 7 + [_U32, _U32, _U32, _F, _U32]),
     "launch_paged_mha_decode_kv": (None, [_P] * 5 + [_U32, _U32, _U32, _F, _U32]),
@@ -215,6 +216,27 @@ def attention_backward(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d
                             _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(workspace),
                             workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head, scale,
                             int(bool(causal)), _stream_ptr(stream)))
+    return d_q, d_k, d_v
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # DFATTN_NOALLOC_SCRATCH_BYTES
+
+
+def attention_backward_noalloc(q, k, v, o, d_o, lse, n_heads, scale=None, causal=True, d_q=None, d_k=None,
+                               d_v=None, stream=None):
+    """dfattn_bwd_noalloc: attention_backward with the workspace in the library's static device array
+    (nothing is allocated by the library; pass d_q, d_k, d_v to allocate nothing here either).
+    Calls that overlap on one GPU race on that array."""
+    torch = _torch()
+    seq_len, d_head = _dims(q, n_heads)
+    if scale is None:
+        scale = d_head ** -0.5
+    d_q = torch.empty_like(q) if d_q is None else d_q
+    d_k = torch.empty_like(q) if d_k is None else d_k
+    d_v = torch.empty_like(q) if d_v is None else d_v
+    _check(lib().dfattn_bwd_noalloc(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o), _dev_ptr(lse),
+                                    _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), n_heads, seq_len, d_head, scale,
+                                    int(bool(causal)), _stream_ptr(stream)))
     return d_q, d_k, d_v
 
 

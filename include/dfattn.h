@@ -249,6 +249,25 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                     float scale, uint32_t causal, void *stream);
 
+/* Backward that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot call hipMalloc or take a workspace (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Same arguments, semantics and results as dfattn_bwd without
+ * the workspace: the workspace lives in a static device array of
+ * DFATTN_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until
+ * the process ends. Shapes whose dfattn_bwd_workspace_bytes() exceeds it
+ * (for d_head = 64: n_heads * seq_len above about 63,000, e.g. H = 12,
+ * S = 4096 fits) return DFATTN_ERR_WORKSPACE before any HIP call. Every
+ * call on one GPU uses that GPU's one array: calls that overlap on one GPU
+ * (different streams, or threads) race and give wrong results; serialise
+ * them. Nothing in the array needs to be cleared between calls.           */
+#define DFATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int dfattn_bwd_noalloc(const float *q, const float *k, const float *v,
+                       const float *o, const float *d_o, const float *lse,
+                       float *d_q, float *d_k, float *d_v, uint32_t n_heads,
+                       uint32_t seq_len, uint32_t d_head, float scale,
+                       uint32_t causal, void *stream);
+
 /* Decode on a stream with a status: the five launchers above in one entry
  * point. block_table NULL: contiguous cache (page_size ignored); kv_dtype
  * DFATTN_KV_F32 or DFATTN_KV_BF16 (k_cache, v_cache then point to uint16

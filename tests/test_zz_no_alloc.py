@@ -1,0 +1,64 @@
+"""dfattn_bwd_noalloc: the backward whose workspace is the library's static device array.
+
+GPU: two calls in a row (the second on a smaller shape, which reuses the array the first left
+filled) give dfattn_bwd's gradients bit for bit (the same kernels on the same inputs). The HIP
+runtime places the static array in device memory when the library first looks up its address,
+so the first call in a process may lower the device's free memory by the array's size; the
+second call changes no device memory figure (hipMemGetInfo). CPU: a shape whose workspace
+exceeds the array is rejected before any HIP call.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import dfattn
+import oracle as O
+
+
+def say(msg):
+    print(f"[no-alloc] {msg}", flush=True)
+
+
+def test_rejects_shapes_beyond_the_static_scratch():
+    lib = dfattn.lib()
+    fake = ctypes.c_void_p(0x10000)  # never dereferenced: the size check fails first
+    need = lib.dfattn_bwd_workspace_bytes(12, 8192, 64)
+    assert need > dfattn.NOALLOC_SCRATCH_BYTES
+    st = lib.dfattn_bwd_noalloc(*([fake] * 9), 12, 8192, 64, 0.125, 1, None)
+    assert st == -6
+    assert b"static scratch" in lib.dfattn_last_error_message()
+    assert lib.dfattn_bwd_workspace_bytes(12, 4096, 64) <= dfattn.NOALLOC_SCRATCH_BYTES
+    lib.dfattn_clear_error()
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_dfattn_bwd_on_two_calls(device):
+    import torch
+
+    for call, (seq_len, seed) in enumerate(((4096, 12100), (1000, 12200))):
+        say(f"H=12 S={seq_len} seed {seed}: dfattn_bwd, then dfattn_bwd_noalloc")
+        x = O.seeded_inputs(seq_len, 12, 64, seed)
+        q, k, v, g = (torch.from_numpy(x[n]).to(device) for n in ("q", "k", "v", "do"))
+        o, lse = dfattn.attention_forward(q, k, v, 12, 0.125, True)
+        ref = dfattn.attention_backward(q, k, v, o, g, lse, 12, 0.125, True)
+        got = [torch.full_like(q, float("nan")) for _ in range(3)]
+        torch.cuda.synchronize()
+        free_before, _ = torch.cuda.mem_get_info()
+        dfattn.attention_backward_noalloc(q, k, v, o, g, lse, 12, 0.125, True, *got)
+        torch.cuda.synchronize()
+        free_after, _ = torch.cuda.mem_get_info()
+        say(f"call {call + 1}: device free memory {free_before} -> {free_after}")
+        if call == 0:
+            assert 0 <= free_before - free_after <= dfattn.NOALLOC_SCRATCH_BYTES + (4 << 20), \
+                "the first call took more device memory than the static array"
+        else:
+            assert free_after == free_before, "the no-allocation backward changed the device's free memory"
+        for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+            assert torch.equal(a, b), f"S={seq_len} {name}: differs from dfattn_bwd"
+        if seq_len <= 1000:
+            want = O.backward(x["q"], x["k"], x["v"], x["do"], 12, 0.125, True, threads=8)
+            for name, a, w in zip(("dq", "dk", "dv"), got, want):
+                err = float(np.max(np.abs(a.cpu().numpy().astype(np.float64) - w)))
+                say(f"S={seq_len} {name} max-abs vs oracle {err:.2e}")
+                assert err <= 2e-3
