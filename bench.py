@@ -212,7 +212,7 @@ def kernel_source_hash():
             with open(os.path.join(CSRC, name), "rb") as f:
                 h.update(f.read())
     return h.hexdigest()[:12]
-KERNELS = ("fwd_d64_kernel", "bwd_preprocess_kernel", "bwd_convert_kernel", "bwd_main_kernel")
+KERNELS = ("fwd_d64_kernel", "bwd_prep_kernel", "bwd_main_kernel")
 
 
 def short_kernel_name(name):
@@ -329,7 +329,7 @@ def _gpt2_kernel_class(name):
                        ("adamw_kernel", "AdamW (dfgpt2, one launch over the arena)"),
                        ("step_advance", "AdamW (dfgpt2, one launch over the arena)"),
                        ("bwd_main", "attention backward main (dfattn)"), ("bwd_pre", "attention backward phase 1 (dfattn)"),
-                       ("bwd_convert", "attention backward phase 1 (dfattn)"), ("fusedopti", "AdamW (fused)"),
+                       ("fusedopti", "AdamW (fused)"),
                        ("softmax", "softmax / cross-entropy"), ("nll", "softmax / cross-entropy"),
                        ("layer_norm", "LayerNorm fwd/bwd"), ("gradgammabeta", "LayerNorm fwd/bwd"),
                        ("reduce_kernel", "reductions (bias gradients, sums)"), ("fill", "fills")):

@@ -6,8 +6,11 @@
 // with one atomicAdd per (query, key, d). Here, with no O(S^2) memory and no
 // atomics:
 //
-//  1. bwd_preprocess: Delta_i = dO_i . O_i per (head, row) and the per-block
-//     max |dO| (for a power-of-two operand scale of dO, see below).
+//  1. bwd_prep (one launch, independent 64-row blocks): per block of one
+//     head, a power-of-two scale sigma_b of dO (from the block's max |dO|),
+//     the fp16 copy of sigma_b * dO, Delta_i = dO_i . O_i (scaled by sigma_b,
+//     formed from the rounded copy) and -lse_i * log2(e); without a training
+//     forward also the fp16 copies of c2*Q, K and V.
 //  2. bwd_main, one launch holding two kinds of workgroup, interleaved
 //     longest-first so both fill the chip together:
 //     * dK/dV workgroups own 128 keys of one head (32 per wave, their K and V
@@ -35,63 +38,22 @@
 namespace dfattn {
 namespace {
 
-constexpr int kPreRows = 64;  // rows per preprocess workgroup
-
-// Workspace layout (floats): delta [H*S] | dO block max [H*ceil(S/64)].
-inline size_t ws_delta_floats(int H, int S) { return (size_t)H * S; }
+constexpr int kPreRows = 64;  // rows per phase-1 workgroup (one dO scale per block)
 inline int pre_blocks(int S) { return (S + kPreRows - 1) / kPreRows; }
 
-// Power of two sigma with max|sigma * x| in [8, 16) for amax = max|x|; 1 if
-// amax is 0 or not finite. Both kernels derive sigma from block maxima with
-// this one function.
-__device__ __forceinline__ float pow2_scale(float amax) {
+// Power-of-two scale of a 64-row block of dO: sigma = 2^e with e = 1 (mod 4)
+// and max|sigma * x| in [2, 32) for amax = max|x| (1 if amax is 0 or not
+// finite). fp16 then holds sigma * dO with full precision down to 2^-15 of
+// the block's maximum, and dS = P * (dP - Delta) formed from it keeps well
+// inside the fp16 range. The exponent moves in steps of 4 so that blocks of
+// similar magnitude share one scale (N(0,1) blocks all get 2): the dK/dV
+// accumulators, which add products of many blocks, change units only where
+// the scale changes.
+__device__ __forceinline__ float block_scale(float amax) {
   if (!(amax > 0.f) || !(amax < INFINITY)) return 1.f;
-  const int e = max(-126, min(126, 3 - ilogbf(amax)));
-  return ldexpf(1.f, e);
-}
-
-__device__ __forceinline__ float round_f16(float x) { return (float)(half_t)x; }
-
-// One workgroup (256 threads) handles kPreRows = 64 rows of one head, d_head
-// = 64: thread t owns row t/4 and columns 16*(t%4) .. 16*(t%4)+15.
-// Delta of a row is summed from fp16(sigma_b * dO) * O / sigma_b, sigma_b the
-// block's own scale. The main kernel rounds sigma_h * dO with the head's
-// sigma_h <= sigma_b, both powers of two, so both roundings agree wherever
-// sigma_h * dO is an fp16 normal number.
-__global__ __launch_bounds__(256) void bwd_preprocess_kernel(
-    const float *__restrict__ O, const float *__restrict__ dO, float *__restrict__ delta,
-    float *__restrict__ blockmax, int H, int S) {
-  __shared__ float wmax[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int head = blockIdx.y;
-  const int row = blockIdx.x * kPreRows + (tid >> 2);
-  const bool ok = row < S;
-  const size_t base = ok ? (size_t)row * H * 64 + (size_t)head * 64 + (tid & 3) * 16 : 0;
-  float4 g[4], o[4];
-  float mx = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    g[i] = load4_or_zero(dO + base + 4 * i, ok);
-    o[i] = load4_or_zero(O + base + 4 * i, ok);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(g[i].x), fabsf(g[i].y)), fmaxf(fabsf(g[i].z), fabsf(g[i].w))));
-  }
-  mx = wave_max(mx);
-  if (lane == 0) wmax[wave] = mx;
-  __syncthreads();
-  const float bmax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const float sig = pow2_scale(bmax);
-  float acc = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc += round_f16(g[i].x * sig) * o[i].x;
-    acc += round_f16(g[i].y * sig) * o[i].y;
-    acc += round_f16(g[i].z * sig) * o[i].z;
-    acc += round_f16(g[i].w * sig) * o[i].w;
-  }
-  acc += __shfl_xor(acc, 1, 64);
-  acc += __shfl_xor(acc, 2, 64);
-  if (ok && (tid & 3) == 0) delta[(size_t)head * S + row] = acc / sig;
-  if (tid == 0) blockmax[(size_t)head * gridDim.x + blockIdx.x] = bmax;
+  const int e_fine = 3 - ilogbf(amax);  // max|2^e_fine x| in [8, 16)
+  const int e = e_fine - 2 + (((3 - e_fine) % 4) + 4) % 4;  // the one e = 1 (mod 4) in [e_fine - 2, e_fine + 1]
+  return ldexpf(1.f, max(-123, min(125, e)));
 }
 
 constexpr int kWaves = 8;
@@ -106,11 +68,13 @@ constexpr int kTile = 64 * kD;      // halves per staged [64][64] tile
 // [64][64] tile: thread t takes row t/8, granule t%8.
 static_assert(64 * kD / 8 == kThreads, "one granule per thread per staged tile");
 // LDS ring of kStages stages, each two fp16 tiles (Q and dO, or K and V) and,
-// for the dK/dV path, the block's two row statistics. After the loop the same
+// for the dK/dV path, the block's two row statistics and its dO scale (first
+// value of a 64-float slot). After the loop the same
 // bytes carry the partner waves' partial results (8 waves x 32 registers x 64
 // lanes fp32).
 constexpr int kStages = 4;
-constexpr int kStageBytes = 2 * kTile * 2 + 2 * kQBlock * 4;
+constexpr int kStageBytes = 2 * kTile * 2 + 3 * kQBlock * 4;
+constexpr int kStageSigma = 2 * kTile * 2 + 2 * kQBlock * 4;  // byte offset of the block's dO scale
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kMergeBytes = 8 * 32 * 64 * 4;
 // After the ring: the workgroup's own 128 rows of K and V (dK/dV path) or of
@@ -127,22 +91,20 @@ constexpr int kRowStatOffset = kLdsBytes - kRowStatBytes;
 template <int N>
 using Const = std::integral_constant<int, N>;
 
-// Workspace layout (bytes): Delta [H*S] fp32 | dO block max [H*ceil(S/64)]
-// fp32 | then, 256-byte aligned, sigma of every head [H] fp32, the row
-// statistics as the main kernel's products take them, -lse*log2(e) and
-// -Delta*sigma, each [H][S] fp32, and the fp16 copies c2*Q, K, V and
-// sigma*dO, each [H][S][64].
+// Workspace layout (bytes, each part 256-byte aligned): the dO scale of
+// every 64-row block, sigma [H][ceil(S/64)] fp32; the row statistics as the
+// main kernel's products take them, -lse*log2(e) and -Delta*sigma_b, each
+// [H][S] fp32; the fp16 copies c2*Q, K, V and sigma_b*dO, each [H][S][64].
 struct WsLayout {
-  size_t blockmax, sigma, lse2n, deltan, q16, k16, v16, do16, total;
+  size_t sigma, lse2n, deltan, q16, k16, v16, do16, total;
 };
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 inline WsLayout ws_layout(int H, int S) {
   WsLayout w;
-  w.blockmax = ws_delta_floats(H, S) * sizeof(float);
   const size_t stat = align256((size_t)H * S * sizeof(float));
   const size_t copy = align256((size_t)H * S * kD * sizeof(half_t));
-  w.sigma = align256(w.blockmax + (size_t)H * pre_blocks(S) * sizeof(float));
-  w.lse2n = align256(w.sigma + (size_t)H * sizeof(float));
+  w.sigma = 0;
+  w.lse2n = align256((size_t)H * pre_blocks(S) * sizeof(float));
   w.deltan = w.lse2n + stat;
   w.q16 = w.deltan + stat;
   w.k16 = w.q16 + copy;
@@ -152,56 +114,85 @@ inline WsLayout ws_layout(int H, int S) {
   return w;
 }
 
-// fp16 copies and row statistics for the main kernel: 64 rows of one head
-// per workgroup (256 threads; thread t converts row t/4, columns
-// 16*(t%4) .. +15 of each tensor). c2*Q is rounded as the forward rounds its Q (round_scaled4);
-// sigma is the head's power of two from the preprocess block maxima, so
-// sigma*dO is exact in fp32 and rounds as the preprocess rounded it for
-// Delta wherever sigma*dO is an fp16 normal number.
-__global__ __launch_bounds__(256) void bwd_convert_kernel(
+// Phase 1: 64 rows of one head per workgroup (256 threads; thread t owns row
+// t/4, columns 16*(t%4) .. +15 of each tensor). The block's dO scale sigma_b
+// comes from the block's own max |dO|, so blocks are independent and phase 1
+// is one launch. Delta is summed from the same rounded sigma_b * dO that the
+// main kernel's dP products use, so the rows of dS = P * (dP - Delta) sum to
+// zero for the rounded operands. Without a training forward (convert_qkv)
+// the workgroup also writes c2*Q (rounded as the forward rounds it,
+// round_scaled4), K and V.
+__global__ __launch_bounds__(256) void bwd_prep_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
-    const float *__restrict__ dO, const float *__restrict__ lse, const float *__restrict__ delta,
-    const float *__restrict__ blockmax, float *__restrict__ sigma_out, float *__restrict__ lse2n,
-    float *__restrict__ deltan,
+    const float *__restrict__ O, const float *__restrict__ dO, const float *__restrict__ lse,
+    float *__restrict__ sigma_out, float *__restrict__ lse2n, float *__restrict__ deltan,
     half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
-    int H, int S, int n_pre_blocks, float c2, int convert_qkv) {
-  const int tid = threadIdx.x, lane = tid & 63;
+    int H, int S, float c2, int convert_qkv) {
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
-  const int row = blockIdx.x * 64 + (tid >> 2);
+  const int row = blockIdx.x * kPreRows + (tid >> 2);
   const bool ok = row < S;
   const size_t src = ok ? (size_t)row * H * kD + (size_t)head * kD + (tid & 3) * 16 : 0;
   const size_t dst = ((size_t)head * S + row) * kD + (tid & 3) * 16;
-  // Every load first, then sigma of the head (from the preprocess block
-  // maxima, reduced by every wave), then the conversions.
-  float4 x[4][4];
-  const float *in[4] = {Q, K, V, dO};
+  const size_t r = (size_t)head * S + row;
+  // Every load first.
+  float4 g[4], o[4], x[3][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int i = 0; i < 4; ++i) {
+    g[i] = load4_or_zero(dO + src + 4 * i, ok);
+    o[i] = load4_or_zero(O + src + 4 * i, ok);
+  }
+  const float *in[3] = {Q, K, V};
+  if (convert_qkv) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok && (t == 3 || convert_qkv));
-  float gmax = 0.f;
-  for (int i = lane; i < n_pre_blocks; i += 64) gmax = fmaxf(gmax, blockmax[(size_t)head * n_pre_blocks + i]);
-  const float sigma = pow2_scale(wave_max(gmax));
-  if (blockIdx.x == 0 && tid == 0) sigma_out[head] = sigma;
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok);
+  }
+  const float l = ok ? lse[r] : 0.f;
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(g[i].x), fabsf(g[i].y)), fmaxf(fabsf(g[i].z), fabsf(g[i].w))));
+  mx = wave_max(mx);
+  if (lane == 0) wmax[wave] = mx;
+  __syncthreads();
+  const float sig = block_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+  if (tid == 0) sigma_out[(size_t)head * gridDim.x + blockIdx.x] = sig;
+  // sigma_b * dO in fp16, and Delta from exactly those values.
+  float acc = 0.f;
+  half4_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = to_half4(scale4(g[i], sig));
+    acc += (float)h[i][0] * o[i].x;
+    acc += (float)h[i][1] * o[i].y;
+    acc += (float)h[i][2] * o[i].z;
+    acc += (float)h[i][3] * o[i].w;
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
   if (!ok) return;
   if ((tid & 3) == 0) {
-    const size_t r = (size_t)head * S + row;
-    lse2n[r] = -lse[r] * kLog2e;
-    deltan[r] = -(delta[r] * sigma);
+    lse2n[r] = -l * kLog2e;
+    deltan[r] = -acc;
   }
-  half_t *out[4] = {q16, k16, v16, do16};
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (t < 3 && !convert_qkv) continue;
+  for (int i = 0; i < 2; ++i)
+    *reinterpret_cast<half8_t *>(do16 + dst + 8 * i) = half8_t{h[2 * i][0], h[2 * i][1], h[2 * i][2], h[2 * i][3],
+                                                               h[2 * i + 1][0], h[2 * i + 1][1], h[2 * i + 1][2],
+                                                               h[2 * i + 1][3]};
+  if (!convert_qkv) return;
+  half_t *out[3] = {q16, k16, v16};
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       half4_t lo, hi;
       if (t == 0) {
         lo = round_scaled4(x[t][2 * i], c2);
         hi = round_scaled4(x[t][2 * i + 1], c2);
-      } else if (t == 3) {
-        lo = to_half4(scale4(x[t][2 * i], sigma));
-        hi = to_half4(scale4(x[t][2 * i + 1], sigma));
       } else {
         lo = to_half4(x[t][2 * i]);
         hi = to_half4(x[t][2 * i + 1]);
@@ -209,7 +200,6 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
       *reinterpret_cast<half8_t *>(out[t] + dst + 8 * i) =
           half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-  }
 }
 
 // Relative cost of one step of each item kind (measured at C2: a dK/dV step,
@@ -217,15 +207,15 @@ __global__ __launch_bounds__(256) void bwd_convert_kernel(
 constexpr int kCostKvStep = 32;
 constexpr int kCostQStep = 25;
 
-// The main kernel reads fp16 copies of its inputs, written once by
-// bwd_convert_kernel in [H][S][64] order: c2*Q (c2 = scale*log2(e), the
-// forward's rounding), K, V and sigma*dO (sigma the head's power-of-two
-// scale).
+// The main kernel reads fp16 copies of its inputs, written in [H][S][64]
+// order by phase 1 (or, for c2*Q, K and V, by the training forward): c2*Q
+// (c2 = scale*log2(e), the forward's rounding), K, V and sigma_b*dO (sigma_b
+// the power-of-two scale of the row's 64-row block, sigma [H][n_blocks]).
 struct BwdArgs {
   const half_t *Q16, *K16, *V16, *dO16;
   const float *lse2n, *deltan, *sigma;
   float *dQ, *dK, *dV;
-  int H, S, causal, n_pre_blocks;
+  int H, S, causal, n_blocks;
   float scale;
 };
 
@@ -294,8 +284,6 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int ld = a.H * kD, hoff = head * kD;
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
   const int key = key0 + c;
-  // The head's dO scale (for the output scaling at the end).
-  const float sigma = a.sigma[head];
 
   // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
   // holds its key, slots d = 16*ds + 8*hh + j.
@@ -323,12 +311,13 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         troff[j][db][hf] = tile_tr4_off(16 * (2 * qh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
-  // Direct-to-LDS staging of query block i (its c2*Q and sigma*dO rows and
-  // its two row statistics) into ring stage st: wave w fetches rows 8w ..
-  // 8w+7 of each tile (1 KB; lane l's 16 bytes land at byte 16*l of the
-  // wave's kilobyte, so it fetches the global granule the swizzle places
-  // there); waves 0 and 1 also fetch the 64 values of -lse*log2(e) and
-  // -Delta*sigma. Rows past S read as zeros (they then contribute nothing:
+  // Direct-to-LDS staging of query block i (its c2*Q and sigma_b*dO rows,
+  // its two row statistics and its dO scale) into ring stage st: wave w
+  // fetches rows 8w .. 8w+7 of each tile (1 KB; lane l's 16 bytes land at
+  // byte 16*l of the wave's kilobyte, so it fetches the global granule the
+  // swizzle places there); waves 0 and 1 also fetch the 64 values of
+  // -lse*log2(e) and -Delta*sigma_b, wave 2 the block's scale (and the next
+  // ones', unused). Rows past S read as zeros (they then contribute nothing:
   // their Q and dO rows are zero too).
   auto stage_base = [&](int st) { return lds_raw + st * kStageBytes; };
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -344,15 +333,39 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
     if (wave_u < 2)
       lds_fetch4(sgpr_rsrc((wave_u == 0 ? a.lse2n : a.deltan) + base, (unsigned)rows * 4),
                  lds_addr32(stage_base(st) + 2 * kTile * 2 + wave_u * kQBlock * 4), lane * 4);
+    if (wave_u == 2) {
+      const int qb = first_qb + i;
+      const int left = uniform_clamp0<64>(a.n_blocks - qb);
+      lds_fetch4(sgpr_rsrc(a.sigma + (size_t)head * a.n_blocks + min(qb, a.n_blocks), (unsigned)left * 4),
+                 lds_addr32(stage_base(st) + kStageSigma), lane * 4);
+    }
   };
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
+  // The accumulators hold sigma_cur * (dK, dV), sigma_cur the dO scale of the
+  // blocks added so far; a block with another scale first moves them to its
+  // units (an exact power-of-two product). Every wave sees every block's scale
+  // in the same order, so partners end in the same units.
+  int sig_cur = __float_as_int(1.f);
 
   // One block. `masked`: the block may hold the causal diagonal, so rows
   // below this wave's keys are masked and a wave whose rows are all below
   // its keys skips the block.
   auto compute = [&](int i, int st, bool masked) {
+    const int sig_b = __builtin_amdgcn_readfirstlane(
+        __float_as_int(*reinterpret_cast<const float *>(stage_base(st) + kStageSigma)));
+    if (sig_b != sig_cur) {
+      const float ratio = __int_as_float(sig_b) / __int_as_float(sig_cur);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dk[0][r] *= ratio;
+        dk[1][r] *= ratio;
+        dv[0][r] *= ratio;
+        dv[1][r] *= ratio;
+      }
+      sig_cur = sig_b;
+    }
     const int q0 = (first_qb + i) * kQBlock + qh * 32;  // this wave's first query row
     if (masked && q0 + 31 < key0) return;
     const half_t *qt = reinterpret_cast<const half_t *>(stage_base(st));
@@ -474,8 +487,15 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 
   // dK = scale * dS^T Q = ln2 * dS^T (c2 Q) / sigma, dV = P^T dO / sigma; row
   // r is key key0 + 8*(r/4) + 4*hh + r%4, column d = 32*db + c.
-  const f32x16 *res = qh == 0 ? dk : dv;
+  // (Each wave picks its result by value: a pointer chosen between the two
+  // register arrays would put both in scratch memory.)
+  f32x16 res[2];
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) res[db][r] = qh == 0 ? dk[db][r] : dv[db][r];
   float *out = qh == 0 ? a.dK : a.dV;
+  const float sigma = __int_as_float(sig_cur);
   const float out_scale = qh == 0 ? kLn2 / sigma : 1.f / sigma;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -498,8 +518,6 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
   const int q_w0 = q_blk0 + qg * 32;
   const int query = q_w0 + c;
-  // The head's dO scale (for the output scaling at the end).
-  const float sigma = a.sigma[head];
   const bool q_ok = query < S;
   const bool wave_active = q_w0 < S;
   const int wave_qlast = min(q_w0 + 32, S) - 1;
@@ -699,8 +717,10 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const f32x16 give[1] = {kh == 0 ? dq[1] : dq[0]};
   exchange_pair<1>(reinterpret_cast<float *>(lds_raw), wave, lane, res, give);
 
-  // dQ = scale * dS K / sigma; register r of block db is column 32*db + 8*(r/4) + 4*hh + r%4.
+  // dQ = scale * dS K / sigma_b, sigma_b the dO scale of the wave's 64-row
+  // block; register r of block db is column 32*db + 8*(r/4) + 4*hh + r%4.
   if (q_ok) {
+    const float sigma = a.sigma[(size_t)head * a.n_blocks + q_w0 / kPreRows];
     const float dq_scale = a.scale / sigma;
     float *qrow = a.dQ + (size_t)query * ld + hoff + kh * 32;
 #pragma unroll
@@ -797,18 +817,12 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                               float scale, hipStream_t stream, bool qkv_saved) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
-  float *delta = reinterpret_cast<float *>(ws);
-  float *blockmax = reinterpret_cast<float *>(ws + w.blockmax);
-  hipLaunchKernelGGL(bwd_preprocess_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream,
-                     o, d_o, delta, blockmax, n_heads, seq_len);
-  if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
-  hipLaunchKernelGGL(bwd_convert_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v,
-                     d_o, lse, delta, blockmax, reinterpret_cast<float *>(ws + w.sigma),
-                     reinterpret_cast<float *>(ws + w.lse2n),
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v, o, d_o,
+                     lse, reinterpret_cast<float *>(ws + w.sigma), reinterpret_cast<float *>(ws + w.lse2n),
                      reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
                      reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
-                     reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, pre_blocks(seq_len),
-                     scale * kLog2e, qkv_saved ? 0 : 1);
+                     reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, scale * kLog2e,
+                     qkv_saved ? 0 : 1);
   return hipGetLastError();
 }
 
@@ -830,7 +844,7 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
   a.H = n_heads;
   a.S = seq_len;
   a.causal = causal ? 1 : 0;
-  a.n_pre_blocks = pre_blocks(seq_len);
+  a.n_blocks = pre_blocks(seq_len);
   a.scale = scale;
   Sched sched;
   sched.n_qblocks = (seq_len + kQBlock - 1) / kQBlock;

@@ -208,10 +208,11 @@ int dfattn_fwd_train(const float *q, const float *k, const float *v, float *o,
                      float scale, uint32_t causal, void *stream);
 
 /* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len * d_head)
- * (row statistics Delta_i = dO_i . O_i, a per-head dO range scale, the row
- * statistics as the main phase's products take them, and fp16 copies of the
- * scaled Q, K, V and dO that the main phase reads; 8 bytes per element of
- * one input, 25 MB at H = 12, S = 4096, D = 64).
+ * (a power-of-two dO scale per 64-row block, the row statistics -lse*log2(e)
+ * and -Delta_i (Delta_i = dO_i . O_i) as the main phase's products take
+ * them, and fp16 copies of the scaled Q, K, V and dO that the main phase
+ * reads; 8 bytes per element of one input, 25 MB at H = 12, S = 4096,
+ * D = 64).
  * Returns 0 when the arguments are invalid.                                */
 size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len,
                                   uint32_t d_head);
