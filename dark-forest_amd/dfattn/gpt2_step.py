@@ -1,6 +1,6 @@
 """GPT-2 training step around the fused attention: the harness that reports "GPT-2 step ms".
 
-Mirrors the reference's static engine step (darkforest-core/src/engine/static_gpt2.rs):
+Mirrors the reference's static engine (darkforest-core/src/engine/static_gpt2.rs):
 
 * model (static_gpt2.rs:276-567): learned token and position embeddings, L
   pre-LayerNorm blocks (LN eps 1e-5, darkforest-cuda/kernels/layernorm.cu:14),
@@ -11,20 +11,23 @@ Mirrors the reference's static engine step (darkforest-core/src/engine/static_gp
   biases 0 — drawn from a seeded generator (the reference's thread_rng is
   unseeded, static_gpt2.rs:264-271);
 * step (static_gpt2.rs:1375-1696): forward, mean cross-entropy over the S
-  positions, backward, AdamW with beta (0.9, 0.95), eps 1e-8 and weight decay
-  0.1 on every parameter (static_gpt2.rs:518-521; update rule lib.rs:1755-1788);
-* attention: per layer the fused causal kernel with scale (d_model/H)^-0.5
-  (static_gpt2.rs:1291, 1329-1336, 1500-1510) — here dfattn's fast path through
-  FusedCausalAttention, which keeps the forward's O and logsumexp for the
-  backward.
+  positions in chunks of at most 512 rows, backward, AdamW with beta (0.9, 0.95),
+  eps 1e-8 and weight decay 0.1 on every parameter (static_gpt2.rs:518-521;
+  update rule lib.rs:1755-1788);
+* attention: per layer one dfattn AttentionContext (static_gpt2.rs:401-406) whose
+  forward_device_into / backward_device_into the step calls with the layer's
+  retained q, k, v (static_gpt2.rs:1329-1336, 1500-1510) and scale (d_model/H)^-0.5
+  (static_gpt2.rs:1291, 1439).
 
-On the GPU the step's other kernels are this library's too (dfattn.ops, include/dfgpt2.h):
-LayerNorm forward and backward, tanh GELU, the linear layers' bias gradients and AdamW over one
-arena holding every weight, gradient and moment (the engine's single allocation), all fp32; the
-GEMMs are hipBLASLt fp32. On the CPU (the checkpoint tests' twin) the same model runs on PyTorch's
-operators and optimizer. `attention="sdpa"`
-swaps in torch's scaled_dot_product_attention (the reference's own parity
-comparator, scripts/verify_loss_parity.py:58) for loss-parity checks.
+On the GPU (attention="dfattn") the step is the engine's own explicit forward and backward, with no
+autograd: every activation and backward scratch buffer is a view of one allocation sized at
+construction (`_NativeEngine`), the weights, gradients and AdamW moments are one more
+(`ops.ParamArena`), and every kernel but the GEMMs is this library's (include/dfgpt2.h and the
+attention contexts): embedding gather and gradient, LayerNorm, tanh GELU, the bias gradients, the
+chunked fused cross-entropy and one AdamW launch over the whole arena, all fp32; the GEMMs are
+hipBLASLt fp32. attention="sdpa", and any model on the CPU, is the reference's own parity comparator
+instead (scripts/verify_loss_parity.py:58): the same model in plain PyTorch operators with torch's
+scaled_dot_product_attention and torch's AdamW, differentiated by autograd.
 """
 from __future__ import annotations
 
@@ -32,7 +35,7 @@ import math
 import struct
 import time
 
-from . import FusedCausalAttention
+from . import AttentionContext
 from . import ops as _ops
 
 
@@ -40,6 +43,11 @@ def _torch():
     import torch
 
     return torch
+
+
+def _f32(x):
+    """The float32 value of x (the engine keeps its hyper-parameters as f32, static_gpt2.rs:518-521)."""
+    return struct.unpack("<f", struct.pack("<f", x))[0]
 
 
 class StaticGPT2:
@@ -84,20 +92,18 @@ class StaticGPT2:
         self.ln_f_g = const(1, d_model)
         self.ln_f_b = const(0, d_model)
         self.lm_head = randn(vocab_size, d_model)
-        # The engine keeps its hyper-parameters as f32 (static_gpt2.rs:518-521), which its checkpoint
-        # footer stores; holding the same f32 values makes a resumed run continue bit for bit.
-        f32 = lambda x: struct.unpack("<f", struct.pack("<f", x))[0]  # noqa: E731
-        # On the GPU: one arena for weights, gradients and moments, the AdamW update in one launch
-        # (the engine's update is one kernel per tensor, lib.rs:1755-1788), the step count on the
-        # device, so a step can always be recorded into a graph. On the CPU: torch's AdamW.
-        self.native = self.device.type == "cuda"
-        hp = dict(lr=f32(lr), betas=(f32(0.9), f32(0.95)), eps=f32(1e-8), weight_decay=f32(0.1))
+        # Holding the same f32 hyper-parameters as the engine's checkpoint footer makes a resumed
+        # run continue bit for bit.
+        hp = dict(lr=_f32(lr), betas=(_f32(0.9), _f32(0.95)), eps=_f32(1e-8), weight_decay=_f32(0.1))
+        self.native = self.device.type == "cuda" and attention == "dfattn"
         if self.native:
             arena = _ops.ParamArena(self.parameters(), self.device)
             self._rebind(arena.adopt(self.parameters()))
             self.opt = _ops.ArenaAdamW(arena, self.parameters(), **hp)
+            self._engine = _NativeEngine(self)
         else:
             self.opt = torch.optim.AdamW(self.parameters(), **hp, capturable=capturable)
+            self._engine = None
         self._graph = None
 
     def parameters(self):
@@ -122,57 +128,48 @@ class StaticGPT2:
             for a, b in zip(self.parameters(), other.parameters()):
                 a.copy_(b)
 
-    def _attention(self, q, k, v):
+    # ------------------------------------------------------------ the PyTorch comparator
+    def _torch_loss(self, tokens, targets):
+        """Mean cross-entropy of one sequence in plain PyTorch operators (autograd-differentiable)."""
         torch = _torch()
-        scale = (self.d_model / self.n_heads) ** -0.5
-        if self.attention == "dfattn":
-            return FusedCausalAttention.apply(q, k, v, self.n_heads, scale, True)
-        s, h, d = q.shape[0], self.n_heads, self.d_model // self.n_heads
-        qh, kh, vh = (t.view(s, h, d).transpose(0, 1).contiguous() for t in (q, k, v))
-        o = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
-        return o.transpose(0, 1).reshape(s, h * d)
-
-    def loss(self, tokens, targets):
-        """Mean cross-entropy of one sequence (static_gpt2.rs:1386-1418)."""
-        F = _torch().nn.functional
-        if self.native:
-            # the parameter gradients go straight into the arena (ops: direct accumulation)
-            ln = lambda t, g, b: _ops.layer_norm(t, g, b, direct=True)  # noqa: E731
-            lin = lambda t, w, b=None: _ops.linear(t, w, b, direct=True)  # noqa: E731
-            gelu = _ops.gelu
-            x = _ops.embedding(self.tok_emb, tokens, direct=True)
-        else:
-            d = self.d_model
-            ln = lambda t, g, b: F.layer_norm(t, (d,), g, b, 1e-5)  # noqa: E731
-            lin, gelu = F.linear, lambda t: F.gelu(t, approximate="tanh")  # noqa: E731
-            x = self.tok_emb[tokens]
-        x = x + self.pos_emb[:tokens.shape[0]]
+        F = torch.nn.functional
+        d, h = self.d_model, self.n_heads
+        scale = (d / h) ** -0.5
+        s = tokens.shape[0]
+        x = self.tok_emb[tokens] + self.pos_emb[:s]
         for lw in self.layers:
-            h = ln(x, lw["ln1_g"], lw["ln1_b"])
-            q = lin(h, lw["wq"], lw["bq"])
-            k = lin(h, lw["wk"], lw["bk"])
-            v = lin(h, lw["wv"], lw["bv"])
-            x = x + lin(self._attention(q, k, v), lw["wo"], lw["bo"])
-            h = ln(x, lw["ln2_g"], lw["ln2_b"])
-            x = x + lin(gelu(lin(h, lw["w1"], lw["b1"])), lw["w2"], lw["b2"])
-        h = ln(x, self.ln_f_g, self.ln_f_b)
-        return F.cross_entropy(lin(h, self.lm_head), targets)
+            y = F.layer_norm(x, (d,), lw["ln1_g"], lw["ln1_b"], 1e-5)
+            q, k, v = (F.linear(y, lw[w], lw[b]) for w, b in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
+            qh, kh, vh = (t.view(s, h, d // h).transpose(0, 1).contiguous() for t in (q, k, v))
+            o = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
+            x = x + F.linear(o.transpose(0, 1).reshape(s, d), lw["wo"], lw["bo"])
+            y = F.layer_norm(x, (d,), lw["ln2_g"], lw["ln2_b"], 1e-5)
+            x = x + F.linear(F.gelu(F.linear(y, lw["w1"], lw["b1"]), approximate="tanh"), lw["w2"], lw["b2"])
+        y = F.layer_norm(x, (d,), self.ln_f_g, self.ln_f_b, 1e-5)
+        return F.cross_entropy(F.linear(y, self.lm_head), targets)
+
+    # ------------------------------------------------------------ public step API
+    def loss(self, tokens, targets):
+        """Mean cross-entropy of one sequence, without an optimizer step (static_gpt2.rs:1386-1418)."""
+        if self.native:
+            return self._engine.forward_loss(tokens, targets).clone()
+        return self._torch_loss(tokens, targets)
 
     def step(self, tokens, targets):
         """One training step: forward, loss, backward, AdamW. Returns the loss tensor (not synchronised)."""
+        if self.native:
+            return self._engine.step(tokens, targets)
         self.opt.zero_grad(set_to_none=False)
-        loss = self.loss(tokens, targets)
+        loss = self._torch_loss(tokens, targets)
         loss.backward()
         self.opt.step()
         return loss.detach()
 
-
     def capture(self, tokens, targets, warmup=3):
         """Record one whole training step into a HIP graph (the engine replays a captured step too,
-        static_gpt2.rs graph_exec) after `warmup` eager steps on a side stream, which allocate the
-        optimizer state and the autograd buffers. Returns the static loss tensor every replay() updates.
-        On the CPU it needs capturable=True (the GPU optimizer always keeps its step count on the
-        device). The batch is copied into static buffers; set_batch() changes it."""
+        static_gpt2.rs graph_exec) after `warmup` eager steps on a side stream. Returns the static
+        loss tensor every replay() updates. The comparator needs capturable=True. The batch is copied
+        into static buffers; set_batch() changes it."""
         torch = _torch()
         if not self.opt.param_groups[0]["capturable"]:
             raise ValueError("StaticGPT2.capture needs capturable=True")
@@ -198,6 +195,224 @@ class StaticGPT2:
             raise RuntimeError("StaticGPT2.replay before capture")
         self._graph.replay()
         return self._loss
+
+    def activation_bytes(self):
+        """Bytes of the native engine's single activation allocation (0 for the comparator)."""
+        return self._engine.arena_bytes if self.native else 0
+
+
+class _NativeEngine:
+    """The step of static_gpt2.rs:1286-1696 on preallocated buffers.
+
+    Every activation the backward needs and every backward scratch tensor is a view of one flat
+    float32 allocation made here (the engine's arena, static_gpt2.rs:401-567), each view starting
+    on a 256-byte boundary; token ids, targets and positions are one int32 allocation. Per layer the
+    step keeps x_in, the LayerNorm outputs and statistics, q, k, v, the attention output, x_mid and
+    both MLP activations, as the reference's LayerActs do (static_gpt2.rs:45-60); the backward
+    scratch (static_gpt2.rs:61-74) is shared by all layers. Each layer's AttentionContext reuses
+    its forward in the backward (the q, k, v and output views are not touched in between).
+    """
+
+    def __init__(self, m: StaticGPT2):
+        torch = _torch()
+        self.m = m
+        S, d, F, V, L, H = m.seq_len, m.d_model, m.d_ff, m.vocab_size, m.n_layers, m.n_heads
+        self.chunk = min(S, 512)  # static_gpt2.rs:423
+        dev = m.device
+        plan = []  # (name, shape)
+
+        def buf(name, *shape):
+            plan.append((name, shape))
+
+        for l in range(L + 1):
+            buf(f"x{l}", S, d)
+        for l in range(L):
+            for n in ("ln1", "q", "k", "v", "att", "xmid", "ln2"):
+                buf(f"{n}{l}", S, d)
+            buf(f"st1{l}", 2, S)
+            buf(f"st2{l}", 2, S)
+            buf(f"h{l}", S, F)
+            buf(f"a{l}", S, F)
+        buf("lnf", S, d)
+        buf("stf", 2, S)
+        buf("tmp", S, d)
+        buf("logits", self.chunk, V)
+        buf("row_loss", S)
+        buf("loss", 1)
+        for n in ("g0", "g1", "dlnf", "dln", "datt", "dq", "dk", "dv"):
+            buf(n, S, d)
+        buf("dh", S, F)
+        buf("da", S, F)
+        offsets, n = {}, 0
+        for name, shape in plan:
+            size = 1
+            for s in shape:
+                size *= s
+            offsets[name] = (n, shape, size)
+            n += (size + 63) // 64 * 64
+        self.arena = torch.empty(n, dtype=torch.float32, device=dev)
+        self.arena_bytes = n * 4
+        self.b = {name: self.arena[o:o + size].view(shape) for name, (o, shape, size) in offsets.items()}
+        ints = torch.empty(3 * ((S + 63) // 64 * 64), dtype=torch.int32, device=dev)
+        w = (S + 63) // 64 * 64
+        self.ids, self.tgt, self.pos = ints[:S], ints[w:w + S], ints[2 * w:2 * w + S]
+        self.pos.copy_(torch.arange(S, dtype=torch.int32, device=dev))
+        self.ctx = [AttentionContext(H, S, d // H, reuse_forward=True) for _ in range(L)]
+        self.scale = (d / H) ** -0.5
+
+    # ---------------------------------------------------------------- pieces
+    @staticmethod
+    def _linear(x, w, b, out):
+        """out = x W^T + b (static_gpt2.rs linear_into; hipBLASLt)."""
+        _torch().addmm(b, x, w.t(), out=out)
+
+    @staticmethod
+    def _linear_backward(x, w, dy, dx, accumulate_dx=False):
+        """dx (=|+=) dy W; W's gradient = dy^T x and the bias's = column sums of dy, into the arena
+        gradient views (static_gpt2.rs linear_backward_into / _accumulate_into)."""
+        torch = _torch()
+        if dx is not None:
+            if accumulate_dx:
+                dx.addmm_(dy, w)
+            else:
+                torch.mm(dy, w, out=dx)
+        torch.mm(dy.t(), x, out=w.grad)
+
+    @staticmethod
+    def _bias_grad(dy, b):
+        rows, n = dy.shape
+        _ops._check(_ops.ops_lib().dfgpt2_linear_grad_bias(_ops._dev_ptr(dy), _ops._dev_ptr(b.grad), rows, n, 0,
+                                                           _ops._stream_ptr()))
+
+    @staticmethod
+    def _ln(x, g, b, out, stats):
+        rows, f = x.shape
+        _ops._check(_ops.ops_lib().dfgpt2_layernorm_forward(
+            _ops._dev_ptr(x), _ops._dev_ptr(g), _ops._dev_ptr(b), _ops._dev_ptr(out), _ops._dev_ptr(stats[0]),
+            _ops._dev_ptr(stats[1]), rows, f, _ops._stream_ptr()))
+
+    @staticmethod
+    def _ln_backward(dy, x, g, b, stats, dx):
+        """dx overwritten; gamma's and beta's gradients added into their (zeroed) arena views."""
+        rows, f = x.shape
+        _ops._check(_ops.ops_lib().dfgpt2_layernorm_backward(
+            _ops._dev_ptr(dy), _ops._dev_ptr(x), _ops._dev_ptr(g), _ops._dev_ptr(stats[0]), _ops._dev_ptr(stats[1]),
+            _ops._dev_ptr(dx), _ops._dev_ptr(g.grad), _ops._dev_ptr(b.grad), rows, f, _ops._stream_ptr()))
+
+    def _set_batch(self, tokens, targets):
+        if tokens.shape[0] != self.m.seq_len or targets.shape[0] != self.m.seq_len:
+            raise ValueError(f"the engine runs sequences of exactly seq_len = {self.m.seq_len} tokens")
+        self.ids.copy_(tokens)
+        self.tgt.copy_(targets)
+
+    # ---------------------------------------------------------------- forward (static_gpt2.rs:1286-1373)
+    def _forward(self):
+        torch = _torch()
+        m, b = self.m, self.b
+        S = m.seq_len
+        x0 = b["x0"]
+        _ops.embedding_forward(self.ids, m.tok_emb, x0)
+        torch.add(x0, m.pos_emb[:S], out=x0)  # positions 0..S-1 of the position table
+        for l, lw in enumerate(m.layers):
+            x, ln1, ln2 = b[f"x{l}"], b[f"ln1{l}"], b[f"ln2{l}"]
+            q, k, v, att, xmid = b[f"q{l}"], b[f"k{l}"], b[f"v{l}"], b[f"att{l}"], b[f"xmid{l}"]
+            self._ln(x, lw["ln1_g"], lw["ln1_b"], ln1, b[f"st1{l}"])
+            self._linear(ln1, lw["wq"], lw["bq"], q)
+            self._linear(ln1, lw["wk"], lw["bk"], k)
+            self._linear(ln1, lw["wv"], lw["bv"], v)
+            self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
+            self._linear(att, lw["wo"], lw["bo"], b["tmp"])
+            torch.add(x, b["tmp"], out=xmid)
+            self._ln(xmid, lw["ln2_g"], lw["ln2_b"], ln2, b[f"st2{l}"])
+            self._linear(ln2, lw["w1"], lw["b1"], b[f"h{l}"])
+            _ops._check(_ops.ops_lib().dfgpt2_gelu_forward(_ops._dev_ptr(b[f"h{l}"]), _ops._dev_ptr(b[f"a{l}"]),
+                                                           b[f"a{l}"].numel(), _ops._stream_ptr()))
+            self._linear(b[f"a{l}"], lw["w2"], lw["b2"], b["tmp"])
+            torch.add(xmid, b["tmp"], out=b[f"x{l + 1}"])
+        self._ln(b[f"x{m.n_layers}"], m.ln_f_g, m.ln_f_b, b["lnf"], b["stf"])
+
+    # ---------------------------------------------------------------- loss (static_gpt2.rs:1386-1418)
+    def _loss_and_head_backward(self):
+        """Chunks of at most 512 rows: logits = lnf lm_head^T, the fused cross-entropy (the gradient
+        overwrites the logits in place), then the chunk's share of d(lnf) and of lm_head's
+        gradient; finally the rows' losses summed in order."""
+        torch = _torch()
+        m, b = self.m, self.b
+        S = m.seq_len
+        for start in range(0, S, self.chunk):
+            c = min(self.chunk, S - start)
+            lg = b["logits"][:c]
+            x = b["lnf"][start:start + c]
+            torch.mm(x, m.lm_head.t(), out=lg)
+            _ops.logit_ce_chunk(lg, self.tgt[start:start + c], lg, b["row_loss"][start:start + c], S)
+            torch.mm(lg, m.lm_head, out=b["dlnf"][start:start + c])
+            if start == 0:
+                torch.mm(lg.t(), x, out=m.lm_head.grad)
+            else:
+                m.lm_head.grad.addmm_(lg.t(), x)
+        _ops.sum_into(b["row_loss"], b["loss"])
+
+    # ---------------------------------------------------------------- backward (static_gpt2.rs:1424-1575)
+    def _backward(self):
+        torch = _torch()
+        m, b = self.m, self.b
+        L = m.n_layers
+        g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
+        self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g)
+        for l in reversed(range(L)):
+            lw = m.layers[l]
+            # MLP: g is d(x_in[l+1]) = d(mlp out) = d(x_mid) through the residual
+            self._linear_backward(b[f"a{l}"], lw["w2"], g, b["da"])
+            self._bias_grad(g, lw["b2"])
+            _ops._check(_ops.ops_lib().dfgpt2_gelu_backward(_ops._dev_ptr(b["da"]), _ops._dev_ptr(b[f"h{l}"]),
+                                                            _ops._dev_ptr(b["dh"]), b["dh"].numel(),
+                                                            _ops._stream_ptr()))
+            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"])
+            self._bias_grad(b["dh"], lw["b1"])
+            # d(x_mid) = g + LayerNorm 2's gradient
+            self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other)
+            torch.add(other, g, out=other)
+            g, other = other, g
+            # attention: output projection, the fused attention backward, the Q/K/V projections
+            self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"])
+            self._bias_grad(g, lw["bo"])
+            self.ctx[l].backward_device_into(b[f"q{l}"], b[f"k{l}"], b[f"v{l}"], b["datt"], self.scale, True,
+                                             b["dq"], b["dk"], b["dv"])
+            ln1 = b[f"ln1{l}"]
+            self._linear_backward(ln1, lw["wq"], b["dq"], b["dln"])
+            self._linear_backward(ln1, lw["wk"], b["dk"], b["dln"], accumulate_dx=True)
+            self._linear_backward(ln1, lw["wv"], b["dv"], b["dln"], accumulate_dx=True)
+            self._bias_grad(b["dq"], lw["bq"])
+            self._bias_grad(b["dk"], lw["bk"])
+            self._bias_grad(b["dv"], lw["bv"])
+            # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
+            self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other)
+            torch.add(other, g, out=other)
+            g, other = other, g
+        # embeddings (static_gpt2.rs:1559-1574): the token rows, and positions 0..S-1
+        _ops.embedding_backward(self.ids, g, m.tok_emb.grad)
+        _ops.embedding_backward(self.pos, g, m.pos_emb.grad)
+
+    # ---------------------------------------------------------------- public
+    # (The parameters are autograd leaves for the comparator-facing API; the engine differentiates
+    # by hand, so its torch calls run under no_grad.)
+    def forward_loss(self, tokens, targets):
+        with _torch().no_grad():
+            self._set_batch(tokens, targets)
+            self._forward()
+            self._loss_and_head_backward()
+        return self.b["loss"][0]
+
+    def step(self, tokens, targets):
+        """static_gpt2.rs:1375-1696: forward, chunked loss, backward, AdamW; returns the device loss."""
+        with _torch().no_grad():
+            self.m.opt.zero_grad()
+            self._set_batch(tokens, targets)
+            self._forward()
+            self._loss_and_head_backward()
+            self._backward()
+            self.m.opt.step()
+        return self.b["loss"][0]
 
 
 def synthetic_batch(vocab_size, seq_len, seed, device):

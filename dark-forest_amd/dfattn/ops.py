@@ -1,15 +1,16 @@
 """The GPT-2 step's non-attention kernels of libdfattn.so (include/dfgpt2.h) for PyTorch tensors.
 
-* `layer_norm`, `linear`, `gelu`, `embedding`: autograd functions on the HIP kernels — LayerNorm
-  forward and backward (darkforest-cuda/kernels/layernorm.cu:97, 187), the linear layer's bias
-  gradient (matmul.cu:240; the two products of a linear layer stay hipBLASLt GEMMs) and tanh GELU
-  (elementwise.cu:195, 217); with direct=True the parameter gradients are added straight into the
-  arena's gradient buffers;
+* `layer_norm_forward` / `layer_norm_backward`, `gelu_forward` / `gelu_backward`, `bias_grad`: the
+  LayerNorm, tanh GELU and bias-gradient kernels (darkforest-cuda/kernels/layernorm.cu:97, 187;
+  elementwise.cu:195, 217; matmul.cu:240) on fresh output tensors;
+* `logit_ce_chunk` / `sum_into`, `embedding_forward` / `embedding_backward`: the chunked fused
+  cross-entropy (softmax.cu:396) and the token embedding and its gradient (elementwise.cu:268, 291);
 * `ParamArena` / `ArenaAdamW`: the engine's single allocation for its weights, gradients and AdamW
   moments (static_gpt2.rs:401-567) and its AdamW update (matmul.cu:341, lib.rs:1755-1788) as one
   launch over the whole arena, with the step count on the device.
 
-Every reduction adds in a fixed order, so a step is reproducible bit for bit.
+Every reduction adds in a fixed order, so a step is reproducible bit for bit. The GPT-2 engine
+(gpt2_step._NativeEngine) calls these and the C ABI directly.
 """
 from __future__ import annotations
 
@@ -37,6 +38,13 @@ SYMBOLS = {
     "dfgpt2_gelu_backward": (_I, [_P, _P, _P, _SZ, _P]),
     "dfgpt2_linear_grad_bias": (_I, [_P, _P, _U32, _U32, _I, _P]),
     "dfgpt2_adamw_update": (_I, [_P] * 4 + [_SZ] + [_F] * 5 + [_P, _P]),
+    "launch_fused_chunked_logit_ce": (None, [_P] * 4 + [_U32, _U32, _U32]),
+    "launch_embedding_forward": (None, [_P] * 3 + [_U32, _U32]),
+    "launch_embedding_backward": (None, [_P] * 3 + [_U32, _U32]),
+    "dfgpt2_logit_ce_chunk": (_I, [_P] * 4 + [_U32, _U32, _U32, _P]),
+    "dfgpt2_sum": (_I, [_P, _U32, _P, _I, _P]),
+    "dfgpt2_embedding_forward": (_I, [_P] * 3 + [_U32, _U32, _U32, _P]),
+    "dfgpt2_embedding_backward": (_I, [_P] * 3 + [_U32, _U32, _U32, _P]),
 }
 
 _typed = None
@@ -108,132 +116,40 @@ def gelu_backward(grad_out, x):
     return grad_x
 
 
-def _grad_of(t, direct):
-    """The arena gradient buffer of parameter t when the caller asked for direct accumulation."""
-    return t.grad if (direct and t is not None and t.grad is not None) else None
-
-
-def _autograd_functions():
+def _ids_ptr(t):
+    """Token ids: a contiguous int32 device tensor, passed as the kernels' uint32 ids."""
     torch = _torch()
-
-    # direct=True (parameters that are ParamArena views): the backward adds the parameter gradients
-    # straight into their .grad buffers in the arena and returns None for them, instead of returning
-    # fresh tensors that autograd would then add into .grad (one more read-modify-write of every
-    # gradient per step). Each parameter is used once per forward, so the sums are the same.
-
-    class LayerNormFn(torch.autograd.Function):
-        """LayerNorm (eps 1e-5) of [rows, F]: static_gpt2.rs layernorm_into / layernorm_backward_into."""
-
-        @staticmethod
-        def forward(ctx, x, gamma, beta, direct):
-            out, means, rstds = layer_norm_forward(x, gamma, beta)
-            ctx.save_for_backward(x, gamma, means, rstds)
-            ctx.gg, ctx.gb = _grad_of(gamma, direct), _grad_of(beta, direct)
-            return out
-
-        @staticmethod
-        def backward(ctx, grad_out):
-            x, gamma, means, rstds = ctx.saved_tensors
-            grad_out = grad_out.contiguous()
-            if ctx.gg is not None and ctx.gb is not None:
-                rows, f = _rows_cols(x)
-                grad_x = torch.empty_like(x)
-                _check(ops_lib().dfgpt2_layernorm_backward(
-                    _dev_ptr(grad_out), _dev_ptr(x), _dev_ptr(gamma), _dev_ptr(means), _dev_ptr(rstds),
-                    _dev_ptr(grad_x), _dev_ptr(ctx.gg), _dev_ptr(ctx.gb), rows, f, _stream_ptr()))
-                return grad_x, None, None, None
-            return layer_norm_backward(grad_out, x, gamma, means, rstds) + (None,)
-
-    class LinearFn(torch.autograd.Function):
-        """y = x W^T (+ b): GEMMs on hipBLASLt, the bias gradient on dfgpt2_linear_grad_bias."""
-
-        @staticmethod
-        def forward(ctx, x, w, b, direct):
-            ctx.save_for_backward(x, w)
-            ctx.has_bias = b is not None
-            ctx.gw, ctx.gb = _grad_of(w, direct), _grad_of(b, direct)
-            return torch.addmm(b, x, w.t()) if b is not None else x.mm(w.t())
-
-        @staticmethod
-        def backward(ctx, grad_out):
-            x, w = ctx.saved_tensors
-            grad_out = grad_out.contiguous()
-            gx = grad_out.mm(w) if ctx.needs_input_grad[0] else None
-            gw = gb = None
-            if ctx.gw is not None:
-                ctx.gw.addmm_(grad_out.t(), x)
-            elif ctx.needs_input_grad[1]:
-                gw = grad_out.t().mm(x)
-            if ctx.has_bias:
-                if ctx.gb is not None:
-                    rows, n = _rows_cols(grad_out)
-                    _check(ops_lib().dfgpt2_linear_grad_bias(_dev_ptr(grad_out), _dev_ptr(ctx.gb), rows, n, 1,
-                                                             _stream_ptr()))
-                elif ctx.needs_input_grad[2]:
-                    gb = bias_grad(grad_out)
-            return gx, gw, gb, None
-
-    class GeluFn(torch.autograd.Function):
-        """tanh GELU (elementwise.cu:181-240)."""
-
-        @staticmethod
-        def forward(ctx, x):
-            ctx.save_for_backward(x)
-            return gelu_forward(x)
-
-        @staticmethod
-        def backward(ctx, grad_out):
-            (x,) = ctx.saved_tensors
-            return gelu_backward(grad_out.contiguous(), x)
-
-    class EmbeddingFn(torch.autograd.Function):
-        """Rows of a table by token id; the backward adds each row's gradient into the table gradient
-        with the sort-based (deterministic) accumulating index_put."""
-
-        @staticmethod
-        def forward(ctx, w, ids, direct):
-            ctx.save_for_backward(ids)
-            ctx.gw, ctx.shape = _grad_of(w, direct), w.shape
-            return w.index_select(0, ids)
-
-        @staticmethod
-        def backward(ctx, grad_out):
-            (ids,) = ctx.saved_tensors
-            grad_out = grad_out.contiguous()
-            if ctx.gw is not None:
-                ctx.gw.index_put_((ids,), grad_out, accumulate=True)
-                return None, None, None
-            g = torch.zeros(ctx.shape, dtype=grad_out.dtype, device=grad_out.device)
-            g.index_put_((ids,), grad_out, accumulate=True)
-            return g, None, None
-
-    return LayerNormFn, LinearFn, GeluFn, EmbeddingFn
+    if not t.is_cuda or t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError("token ids must be a contiguous int32 device tensor")
+    return ctypes.c_void_p(t.data_ptr())
 
 
-_fns = None
+def logit_ce_chunk(logits, targets, grad, row_loss, total_rows):
+    """dfgpt2_logit_ce_chunk over logits [rows, V] (int32 targets [rows]); grad may be logits itself.
+    Each row's loss goes to row_loss[row]."""
+    rows, v = _rows_cols(logits)
+    _check(ops_lib().dfgpt2_logit_ce_chunk(_dev_ptr(logits), _ids_ptr(targets), _dev_ptr(grad), _dev_ptr(row_loss),
+                                           rows, v, total_rows, _stream_ptr()))
 
 
-def _functions():
-    global _fns
-    if _fns is None:
-        _fns = _autograd_functions()
-    return _fns
+def sum_into(values, out, accumulate=False):
+    """dfgpt2_sum: out (a 1-element tensor) = (out if accumulate) + sum(values), fixed order."""
+    _check(ops_lib().dfgpt2_sum(_dev_ptr(values), values.numel(), _dev_ptr(out), int(bool(accumulate)),
+                                _stream_ptr()))
 
 
-def layer_norm(x, gamma, beta, direct=False):
-    return _functions()[0].apply(x, gamma, beta, direct)
+def embedding_forward(ids, table, out):
+    """dfgpt2_embedding_forward: out[p] = table[ids[p]] (ids past the table give zero rows)."""
+    rows_in_table, dim = _rows_cols(table)
+    _check(ops_lib().dfgpt2_embedding_forward(_ids_ptr(ids), _dev_ptr(table), _dev_ptr(out), ids.numel(), dim,
+                                              rows_in_table, _stream_ptr()))
 
 
-def linear(x, w, b=None, direct=False):
-    return _functions()[1].apply(x, w, b, direct)
-
-
-def gelu(x):
-    return _functions()[2].apply(x)
-
-
-def embedding(w, ids, direct=False):
-    return _functions()[3].apply(w, ids, direct)
+def embedding_backward(ids, grad_out, grad_table):
+    """dfgpt2_embedding_backward: grad_table[ids[p]] += grad_out[p], rows of one id summed in order."""
+    rows_in_table, dim = _rows_cols(grad_table)
+    _check(ops_lib().dfgpt2_embedding_backward(_ids_ptr(ids), _dev_ptr(grad_out), _dev_ptr(grad_table), ids.numel(),
+                                               dim, rows_in_table, _stream_ptr()))
 
 
 class ParamArena:

@@ -37,6 +37,21 @@ void launch_adamw_update(float *parameter, float *first_moment, float *second_mo
                          uint32_t n, float lr, float beta1, float beta2, float eps, float weight_decay,
                          float bias_correction1, float bias_correction2);
 
+/* softmax.cu:396 — cross-entropy over a chunk of rows of logits [chunk_rows, cols]: the row's
+ * softmax p overwrites logits, grad_logits = (p - one_hot(target)) / total_rows, and
+ * *loss += -log(max(p_target, 1e-12)) / total_rows per row (float atomics, as the reference; the
+ * engine zeroes *loss before the first chunk). targets: [chunk_rows] token ids.            */
+void launch_fused_chunked_logit_ce(float *logits, const uint32_t *targets, float *grad_logits, float *loss,
+                                   uint32_t chunk_rows, uint32_t cols, uint32_t total_rows);
+/* elementwise.cu:268 — out[p, :] = weight[indices[p], :] for p < seq_len (ids not range-checked,
+ * as in the reference). elementwise.cu:291 — grad_weight[indices[p], :] += grad_out[p, :]: the
+ * rows of one id are summed in position order by one workgroup (no atomics, reproducible); the
+ * caller zeroes grad_weight first, as the reference's wrapper does (lib.rs:1813).             */
+void launch_embedding_forward(const uint32_t *indices, const float *weight, float *out, uint32_t seq_len,
+                              uint32_t embed_dim);
+void launch_embedding_backward(const uint32_t *indices, const float *grad_out, float *grad_weight,
+                               uint32_t seq_len, uint32_t embed_dim);
+
 /* Stream variants. Pointers must be 4-byte aligned; 16-byte aligned rows with features % 4 == 0
  * take the vectorised kernels. batch == 0 or n == 0 is a no-op (the bias gradient is then zero), and
  * the pointers of an empty tensor may be NULL. */
@@ -56,6 +71,23 @@ int dfgpt2_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t ba
 int dfgpt2_adamw_update(float *parameter, float *first_moment, float *second_moment, const float *gradient,
                         size_t n, float lr, float beta1, float beta2, float eps, float weight_decay, float *step,
                         hipStream_t stream);
+
+/* The chunked cross-entropy on a stream: as launch_fused_chunked_logit_ce, except that the
+ * softmax is not written back (grad_logits may be logits itself, which halves the chunk's write
+ * traffic) and each row's loss, -log(max(p_target, 1e-12)) / total_rows, goes to row_loss[row]
+ * instead of an atomic sum; dfgpt2_sum then adds the rows in a fixed order. Reference
+ * counterpart: softmax.cu:396 as called at static_gpt2.rs:1386-1418.                        */
+int dfgpt2_logit_ce_chunk(float *logits, const uint32_t *targets, float *grad_logits, float *row_loss,
+                          uint32_t chunk_rows, uint32_t cols, uint32_t total_rows, hipStream_t stream);
+/* *out = (accumulate ? *out : 0) + sum of values[0..n) in a fixed order (one workgroup). No
+ * reference counterpart: the reference's loss is an atomic sum.                             */
+int dfgpt2_sum(const float *values, uint32_t n, float *out, int accumulate, hipStream_t stream);
+/* The embedding gather and its gradient on a stream (elementwise.cu:268, 291). Rows whose id is
+ * rows_in_table or more are written as zeros (forward) or skipped (backward).              */
+int dfgpt2_embedding_forward(const uint32_t *indices, const float *table, float *out, uint32_t n_rows,
+                             uint32_t dim, uint32_t rows_in_table, hipStream_t stream);
+int dfgpt2_embedding_backward(const uint32_t *indices, const float *grad_out, float *grad_table, uint32_t n_rows,
+                              uint32_t dim, uint32_t rows_in_table, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,19 @@ ODD = ctypes.c_void_p(0x1002)
     ("dfgpt2_linear_grad_bias", (BUF, BUF, 4, 0, 0, None), ERR_SHAPE),
     ("dfgpt2_adamw_update", (BUF, BUF, BUF, BUF, 16, 1e-3, 0.9, 0.95, 1e-8, 0.1, None, None),
      ERR_NULL),
+    ("dfgpt2_logit_ce_chunk", (BUF, None, BUF, BUF, 4, 100, 4, None), ERR_NULL),
+    ("dfgpt2_logit_ce_chunk", (BUF, BUF, ODD, BUF, 4, 100, 4, None), ERR_MISALIGNED),
+    ("dfgpt2_logit_ce_chunk", (BUF, BUF, BUF, BUF, 4, 0, 4, None), ERR_SHAPE),
+    ("dfgpt2_logit_ce_chunk", (BUF, BUF, BUF, BUF, 4, 100, 0, None), ERR_SHAPE),
+    ("dfgpt2_logit_ce_chunk", (BUF, BUF, BUF, BUF, 2**31, 100, 4, None), ERR_OVERFLOW),
+    ("dfgpt2_logit_ce_chunk", (None, None, None, None, 0, 100, 4, None), OK),
+    ("dfgpt2_sum", (None, 4, BUF, 0, None), ERR_NULL),
+    ("dfgpt2_sum", (BUF, 4, None, 0, None), ERR_NULL),
+    ("dfgpt2_embedding_forward", (BUF, None, BUF, 4, 8, 10, None), ERR_NULL),
+    ("dfgpt2_embedding_forward", (BUF, BUF, BUF, 4, 0, 10, None), ERR_SHAPE),
+    ("dfgpt2_embedding_forward", (None, None, None, 0, 8, 10, None), OK),
+    ("dfgpt2_embedding_backward", (BUF, BUF, ODD, 4, 8, 10, None), ERR_MISALIGNED),
+    ("dfgpt2_embedding_backward", (BUF, BUF, BUF, 2**31, 8, 10, None), ERR_OVERFLOW),
 ])
 def test_argument_errors_are_caught_on_the_host(fn, args, status):
     ops.ops_lib().dfattn_clear_error()
@@ -72,4 +85,11 @@ def test_reference_launcher_records_error_for_darkforest_sync():
     lib.dfattn_clear_error()
     lib.launch_adamw_update(None, BUF, BUF, BUF, 16, 1e-3, 0.9, 0.95, 1e-8, 0.1, 0.1, 0.05)
     assert lib.dfattn_last_error() == ERR_NULL
+    lib.dfattn_clear_error()
+    lib.launch_fused_chunked_logit_ce(BUF, BUF, BUF, None, 4, 100, 4)
+    assert lib.dfattn_last_error() == ERR_NULL
+    lib.dfattn_clear_error()
+    lib.launch_embedding_backward(BUF, None, BUF, 4, 8)
+    assert lib.dfattn_last_error() == ERR_NULL
+    assert "dfgpt2_embedding_backward" in lib.dfattn_last_error_message().decode()
     lib.dfattn_clear_error()

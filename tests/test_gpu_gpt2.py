@@ -24,16 +24,20 @@ def say(msg):
     print(f"[gpu-gpt2] {msg}", flush=True)
 
 
-@pytest.mark.parametrize("n_heads", [4, 2])
-def test_loss_parity_against_sdpa_twin(device, n_heads):
-    """n_heads 4 gives d_head 32 (the exact fp32 kernels); n_heads 2 gives d_head 64, the fp16-operand
-    MFMA forward and backward GPT-2 small uses, held to the same bar across optimizer steps."""
-    say(f"loss parity tiny config, {n_heads} heads (d_head {128 // n_heads})")
-    cfg = dict(vocab_size=500, d_model=128, n_heads=n_heads, n_layers=2, d_ff=512, seq_len=64, lr=1e-3, seed=5)
+@pytest.mark.parametrize("n_heads,seq_len", [(4, 64), (2, 64), (2, 640)])
+def test_loss_parity_against_sdpa_twin(device, n_heads, seq_len):
+    """The engine (HIP kernels, explicit backward, one activation allocation) against the same model
+    in plain PyTorch with SDPA and torch's AdamW. n_heads 4 gives d_head 32 (the exact fp32 attention
+    kernels); n_heads 2 gives d_head 64, the fp16-operand MFMA forward and backward GPT-2 small uses;
+    seq_len 640 splits the loss into two chunks (512 + 128 rows). Same bar across optimizer steps."""
+    say(f"loss parity tiny config, {n_heads} heads (d_head {128 // n_heads}), S={seq_len}")
+    cfg = dict(vocab_size=500, d_model=128, n_heads=n_heads, n_layers=2, d_ff=512, seq_len=seq_len, lr=1e-3,
+               seed=5)
     ours = StaticGPT2(**cfg, attention="dfattn")
     twin = StaticGPT2(**cfg, attention="sdpa")
+    assert ours.native and not twin.native
     twin.load_state(ours)
-    tokens, targets = synthetic_batch(500, 64, 7, device)
+    tokens, targets = synthetic_batch(500, seq_len, 7, device)
     for step in range(5):
         a, b = float(ours.step(tokens, targets)), float(twin.step(tokens, targets))
         say(f"step {step}: dfattn {a:.6f} sdpa {b:.6f}")

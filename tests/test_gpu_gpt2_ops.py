@@ -182,3 +182,102 @@ def test_reference_launchers_match_the_stream_entry_points(device):
     lib.darkforest_sync()
     want, _, _ = _adamw_ref(p0, 0, 0, g.double(), 1e-3, 0.9, 0.95, 1e-8, 0.1, 1)
     close(p.double(), want, 0, 1e-6, "launch_adamw_update")
+
+
+# ---------------------------------------------------------------- cross-entropy (softmax.cu:325-413)
+@pytest.mark.parametrize("rows,vocab", [(512, 50257), (7, 1000), (3, 1)])
+def test_chunked_cross_entropy_matches_torch(device, rows, vocab):
+    """dfgpt2_logit_ce_chunk + dfgpt2_sum against torch's fp64 log-softmax: the gradient
+    (softmax - one_hot) / total_rows per value and the mean loss, with the gradient written to its
+    own buffer and in place; the reference launcher writes the softmax back and sums the loss with
+    atomics."""
+    import torch
+
+    say(f"cross-entropy rows={rows} vocab={vocab}")
+    total = 4 * rows  # the chunk is a quarter of the sequence
+    g = torch.Generator(device="cpu").manual_seed(rows + vocab)
+    logits = (torch.randn(rows, vocab, generator=g) * 2).to(device)
+    targets = torch.randint(0, vocab, (rows,), generator=g, dtype=torch.int32).to(device)
+    lp = torch.log_softmax(logits.double(), dim=1)
+    want_grad = (lp.exp() - torch.nn.functional.one_hot(targets.long(), vocab).double()) / total
+    want_rows = -lp.gather(1, targets.long()[:, None])[:, 0] / total
+    grad = torch.empty_like(logits)
+    row_loss = torch.empty(rows, device=device)
+    loss = torch.empty(1, device=device)
+    ops.logit_ce_chunk(logits, targets, grad, row_loss, total)
+    ops.sum_into(row_loss, loss)
+    torch.cuda.synchronize()
+    close(grad.double(), want_grad, 1e-5, 1e-9, "grad")
+    close(row_loss.double(), want_rows, 1e-5, 1e-8, "row losses")
+    close(loss.double(), want_rows.sum()[None], 1e-5, 1e-8, "loss")
+    # in place: the gradient overwrites the logits, bit for bit the same
+    inplace = logits.clone()
+    ops.logit_ce_chunk(inplace, targets, inplace, row_loss, total)
+    torch.cuda.synchronize()
+    assert torch.equal(inplace, grad)
+    # the reference's launcher: probabilities written back, loss added atomically
+    probs = logits.clone()
+    grad2 = torch.empty_like(logits)
+    loss2 = torch.full((1,), 0.25, device=device)
+    ops.ops_lib().launch_fused_chunked_logit_ce(P(probs), P(targets), P(grad2), P(loss2), rows, vocab, total)
+    torch.cuda.synchronize()
+    close(probs.double(), lp.exp(), 1e-5, 1e-9, "probabilities")
+    assert torch.equal(grad2, grad)
+    close(loss2.double(), 0.25 + want_rows.sum()[None], 1e-5, 1e-8, "atomic loss")
+
+
+# ---------------------------------------------------------------- embedding (elementwise.cu:255-298)
+def test_embedding_forward_and_backward_match_torch(device):
+    """Gather of table rows; the gradient adds every position's row into its token's table row,
+    repeated ids included (fp64 index_add as the reference), accumulating onto what the table
+    gradient held, reproducibly; ids past the table are zero rows / skipped."""
+    import torch
+
+    say("embedding S=1024 d=768, vocab 50257 with repeated ids")
+    g = torch.Generator(device="cpu").manual_seed(99)
+    vocab, dim, seq = 50257, 768, 1024
+    table = torch.randn(vocab, dim, generator=g).to(device)
+    ids = torch.randint(0, 300, (seq,), generator=g, dtype=torch.int32)  # many repeats
+    ids[5] = ids[900] = ids[1023] = 7
+    ids = ids.to(device)
+    out = torch.empty(seq, dim, device=device)
+    ops.embedding_forward(ids, table, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, table.index_select(0, ids.long()))
+    gy = torch.randn(seq, dim, generator=g).to(device)
+    base = torch.randn(vocab, dim, generator=g).to(device) * 0.1
+    gt = base.clone()
+    ops.embedding_backward(ids, gy, gt)
+    want = base.double().index_add(0, ids.long(), gy.double())
+    torch.cuda.synchronize()
+    close(gt.double(), want, 1e-6, 1e-5, "table gradient")
+    again = base.clone()
+    ops.embedding_backward(ids, gy, again)
+    torch.cuda.synchronize()
+    assert torch.equal(again, gt)
+    # positions (unique ids, the position table's gradient)
+    pos = torch.arange(seq, dtype=torch.int32, device=device)
+    gp = torch.zeros(seq, dim, device=device)
+    ops.embedding_backward(pos, gy, gp)
+    torch.cuda.synchronize()
+    assert torch.equal(gp, gy)
+    # ids past the table
+    bad = ids.clone()
+    bad[3] = vocab + 5
+    out2 = torch.empty_like(out)
+    ops.embedding_forward(bad, table, out2)
+    gt2 = torch.zeros(vocab, dim, device=device)
+    ops.embedding_backward(bad, gy, gt2)
+    torch.cuda.synchronize()
+    assert torch.all(out2[3] == 0) and torch.equal(out2[4], out[4])
+    keep = torch.ones(seq, dtype=torch.bool)
+    keep[3] = False
+    want2 = torch.zeros(vocab, dim, dtype=torch.float64).index_add(0, ids.long().cpu()[keep], gy.double().cpu()[keep])
+    close(gt2.double().cpu(), want2, 1e-6, 1e-5, "table gradient, one id past the table")
+    # the reference's launchers on the null stream
+    out3 = torch.empty_like(out)
+    gt3 = base.clone()
+    ops.ops_lib().launch_embedding_forward(P(ids), P(table), P(out3), seq, dim)
+    ops.ops_lib().launch_embedding_backward(P(ids), P(gy), P(gt3), seq, dim)
+    dfattn.darkforest_sync()
+    assert torch.equal(out3, out) and torch.equal(gt3, gt)
