@@ -513,6 +513,9 @@ def main():
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
+    ap.add_argument("--sclk", type=int, default=1,
+                    help="1: sample the shader clock with rocm-smi while the step runs (0 under a profiler, whose "
+                         "preloaded library must not see bench.py start another program)")
     ap.add_argument("--decode-only", type=int, default=-1, metavar="I",
                     help="time only DECODE_CONFIGS[I] (200 calls) and print its row (for rocprofv3)")
     ap.add_argument("--seq-limit", type=int, default=0, metavar="MAX_S",
@@ -671,7 +674,7 @@ def main():
     # The shader clock the kernels ran at (rocm-smi, sampled while the same step runs back to back
     # after the timed region) and the roofline fraction against the peak at that clock
     # (256 CUs x 4096 dense fp16 FLOP/clk/CU).
-    sclk = sample_sclk(step)
+    sclk = sample_sclk(step) if args.sclk else None
     result["sclk_mhz"] = sclk
     if sclk:
         peak_sclk = 256 * 4096 * sclk * 1e6 / 1e12
