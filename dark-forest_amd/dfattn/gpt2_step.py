@@ -54,7 +54,7 @@ class StaticGPT2:
     """GPT-2 with the reference engine's architecture, init and optimizer."""
 
     def __init__(self, vocab_size=50257, d_model=768, n_heads=12, n_layers=12, d_ff=3072, seq_len=1024, lr=3e-4,
-                 seed=0, device="cuda", attention="dfattn", capturable=False):
+                 seed=0, device="cuda", attention="dfattn", capturable=False, fast_gemm=True):
         torch = _torch()
         if d_model % n_heads:
             raise ValueError("d_model must be divisible by n_heads")
@@ -96,6 +96,10 @@ class StaticGPT2:
         # run continue bit for bit.
         hp = dict(lr=_f32(lr), betas=(_f32(0.9), _f32(0.95)), eps=_f32(1e-8), weight_decay=_f32(0.1))
         self.native = self.device.type == "cuda" and attention == "dfattn"
+        # The engine's GEMMs take hipBLASLt's fast fp32 path (torch's allow_tf32 on ROCm): relative
+        # error ~5e-6 on these shapes against 1e-6 for the exact path, far inside the TF32 the
+        # reference's cuBLAS GEMMs use (lib.rs:45-48), and up to 2.3x faster on the lm_head GEMM.
+        self.fast_gemm = fast_gemm
         if self.native:
             arena = _ops.ParamArena(self.parameters(), self.device)
             self._rebind(arena.adopt(self.parameters()))
@@ -237,6 +241,10 @@ class _NativeEngine:
         buf("stf", 2, S)
         buf("tmp", S, d)
         buf("logits", self.chunk, V)
+        # lm_head's input gradient d(lnf) = dlogits lm_head has K = vocab: it runs as a batched
+        # product over `ksplit` slices of the vocabulary into these partial sums, then one sum.
+        self.ksplit = max(1, min(32, V // 256))
+        buf("dx_part", self.ksplit, self.chunk, d)
         buf("row_loss", S)
         buf("loss", 1)
         for n in ("g0", "g1", "dlnf", "dln", "datt", "dq", "dk", "dv"):
@@ -266,16 +274,19 @@ class _NativeEngine:
         """out = x W^T + b (static_gpt2.rs linear_into; hipBLASLt)."""
         _torch().addmm(b, x, w.t(), out=out)
 
-    @staticmethod
-    def _linear_backward(x, w, dy, dx, accumulate_dx=False):
+    def _linear_backward(self, x, w, dy, dx, accumulate_dx=False, exact_dx=False):
         """dx (=|+=) dy W; W's gradient = dy^T x and the bias's = column sums of dy, into the arena
-        gradient views (static_gpt2.rs linear_backward_into / _accumulate_into)."""
+        gradient views (static_gpt2.rs linear_backward_into / _accumulate_into). exact_dx: dx on
+        the exact fp32 GEMM path (the faster one for that shape)."""
         torch = _torch()
         if dx is not None:
+            fast = torch.backends.cuda.matmul.allow_tf32
+            torch.backends.cuda.matmul.allow_tf32 = fast and not exact_dx
             if accumulate_dx:
                 dx.addmm_(dy, w)
             else:
                 torch.mm(dy, w, out=dx)
+            torch.backends.cuda.matmul.allow_tf32 = fast
         torch.mm(dy.t(), x, out=w.grad)
 
     @staticmethod
@@ -345,12 +356,28 @@ class _NativeEngine:
             x = b["lnf"][start:start + c]
             torch.mm(x, m.lm_head.t(), out=lg)
             _ops.logit_ce_chunk(lg, self.tgt[start:start + c], lg, b["row_loss"][start:start + c], S)
-            torch.mm(lg, m.lm_head, out=b["dlnf"][start:start + c])
+            self._head_dx(lg, b["dlnf"][start:start + c])
             if start == 0:
                 torch.mm(lg.t(), x, out=m.lm_head.grad)
             else:
                 m.lm_head.grad.addmm_(lg.t(), x)
         _ops.sum_into(b["row_loss"], b["loss"])
+
+    def _head_dx(self, lg, out):
+        """out = lg lm_head with K = vocab split into `ksplit` slices: one strided batched GEMM
+        (slice j of every row of lg against rows j*Kc .. of lm_head, no copies) into the partial
+        sums, their sum over the slices, and the vocabulary's remainder rows added last. hipBLASLt's
+        single GEMM over K = 50257 keeps few workgroups busy (0.57 ms per 512 rows against 0.15)."""
+        torch = _torch()
+        m = self.m
+        rows, V = lg.shape
+        B = self.ksplit
+        kc = V // B
+        part = self.b["dx_part"][:, :rows]
+        torch.bmm(lg[:, :B * kc].view(rows, B, kc).permute(1, 0, 2), m.lm_head[:B * kc].view(B, kc, -1), out=part)
+        torch.sum(part, dim=0, out=out)
+        if B * kc < V:
+            out.addmm_(lg[:, B * kc:], m.lm_head[B * kc:])
 
     # ---------------------------------------------------------------- backward (static_gpt2.rs:1424-1575)
     def _backward(self):
@@ -367,7 +394,7 @@ class _NativeEngine:
             _ops._check(_ops.ops_lib().dfgpt2_gelu_backward(_ops._dev_ptr(b["da"]), _ops._dev_ptr(b[f"h{l}"]),
                                                             _ops._dev_ptr(b["dh"]), b["dh"].numel(),
                                                             _ops._stream_ptr()))
-            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"])
+            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], exact_dx=True)
             self._bias_grad(b["dh"], lw["b1"])
             # d(x_mid) = g + LayerNorm 2's gradient
             self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other)
@@ -395,23 +422,36 @@ class _NativeEngine:
 
     # ---------------------------------------------------------------- public
     # (The parameters are autograd leaves for the comparator-facing API; the engine differentiates
-    # by hand, so its torch calls run under no_grad.)
+    # by hand, so its torch calls run under no_grad. The GEMM precision setting is scoped to the
+    # engine's own calls and restored afterwards.)
+    def _run(self, fn):
+        torch = _torch()
+        prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = bool(self.m.fast_gemm)
+        try:
+            with torch.no_grad():
+                fn()
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = prev
+
     def forward_loss(self, tokens, targets):
-        with _torch().no_grad():
+        def run():
             self._set_batch(tokens, targets)
             self._forward()
             self._loss_and_head_backward()
+        self._run(run)
         return self.b["loss"][0]
 
     def step(self, tokens, targets):
         """static_gpt2.rs:1375-1696: forward, chunked loss, backward, AdamW; returns the device loss."""
-        with _torch().no_grad():
+        def run():
             self.m.opt.zero_grad()
             self._set_batch(tokens, targets)
             self._forward()
             self._loss_and_head_backward()
             self._backward()
             self.m.opt.step()
+        self._run(run)
         return self.b["loss"][0]
 
 
