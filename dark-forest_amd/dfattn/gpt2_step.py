@@ -50,6 +50,11 @@ def _f32(x):
     return struct.unpack("<f", struct.pack("<f", x))[0]
 
 
+# A layer's parameters in parameters() (and arena) order.
+_PARAM_ORDER = ("ln1_g", "ln1_b", "wq", "wk", "wv", "bq", "bk", "bv", "wo", "bo", "ln2_g", "ln2_b", "w1", "b1", "w2",
+                "b2")
+
+
 class StaticGPT2:
     """GPT-2 with the reference engine's architecture, init and optimizer."""
 
@@ -79,7 +84,7 @@ class StaticGPT2:
         self.pos_emb = randn(seq_len, d_model)
         self.layers = []
         for _ in range(n_layers):
-            self.layers.append({
+            lw = {
                 "ln1_g": const(1, d_model), "ln1_b": const(0, d_model),
                 "wq": randn(d_model, d_model), "bq": const(0, d_model),
                 "wk": randn(d_model, d_model), "bk": const(0, d_model),
@@ -88,7 +93,10 @@ class StaticGPT2:
                 "ln2_g": const(1, d_model), "ln2_b": const(0, d_model),
                 "w1": randn(d_ff, d_model), "b1": const(0, d_ff),
                 "w2": randn(d_model, d_ff, s=std_res), "b2": const(0, d_model),
-            })
+            }
+            # Parameter (and arena) order keeps Q, K, V's weights, and their biases, adjacent, so
+            # the engine runs the three projections as one [3 d_model, d_model] linear layer.
+            self.layers.append({k: lw[k] for k in _PARAM_ORDER})
         self.ln_f_g = const(1, d_model)
         self.ln_f_b = const(0, d_model)
         self.lm_head = randn(vocab_size, d_model)
@@ -231,8 +239,9 @@ class _NativeEngine:
         for l in range(L + 1):
             buf(f"x{l}", S, d)
         for l in range(L):
-            for n in ("ln1", "q", "k", "v", "att", "xmid", "ln2"):
+            for n in ("ln1", "att", "xmid", "ln2"):
                 buf(f"{n}{l}", S, d)
+            buf(f"qkv{l}", 3, S, d)  # q, k, v of the layer, each contiguous [S, d]
             buf(f"st1{l}", 2, S)
             buf(f"st2{l}", 2, S)
             buf(f"h{l}", S, F)
@@ -247,8 +256,10 @@ class _NativeEngine:
         buf("dx_part", self.ksplit, self.chunk, d)
         buf("row_loss", S)
         buf("loss", 1)
-        for n in ("g0", "g1", "dlnf", "dln", "datt", "dq", "dk", "dv"):
+        for n in ("g0", "g1", "dlnf", "dln", "datt"):
             buf(n, S, d)
+        buf("dqkv", 3, S, d)  # the attention backward's dq, dk, dv
+        buf("wide", S, 3 * d)  # [S, 3 d_model]: the fused projection's output, or dq|dk|dv by row
         buf("dh", S, F)
         buf("da", S, F)
         offsets, n = {}, 0
@@ -267,6 +278,27 @@ class _NativeEngine:
         self.pos.copy_(torch.arange(S, dtype=torch.int32, device=dev))
         self.ctx = [AttentionContext(H, S, d // H, reuse_forward=True) for _ in range(L)]
         self.scale = (d / H) ** -0.5
+        # Views of each layer's Q, K, V weights (and biases, and their gradients) as one [3d, d]
+        # ([3d]) tensor: they are adjacent in the parameter arena.
+        self.wqkv, self.bqkv = [], []
+        for lw in m.layers:
+            self.wqkv.append(self._adjacent([lw["wq"], lw["wk"], lw["wv"]]))
+            self.bqkv.append(self._adjacent([lw["bq"], lw["bk"], lw["bv"]]))
+
+    @staticmethod
+    def _adjacent(ts):
+        """The parameters ts, consecutive in memory, as one tensor stacked on dim 0 (its .grad the
+        same view of their gradients)."""
+        torch = _torch()
+        first = ts[0]
+        n = first.numel()
+        for i, t in enumerate(ts):
+            if t.data_ptr() != first.data_ptr() + i * n * 4 or t.grad.data_ptr() != first.grad.data_ptr() + i * n * 4:
+                raise RuntimeError("Q, K, V parameters are not adjacent in the arena")
+        shape = (len(ts) * first.shape[0],) + tuple(first.shape[1:])
+        w = torch.as_strided(first.detach(), shape, first.stride())
+        w.grad = torch.as_strided(first.grad, shape, first.grad.stride())
+        return w
 
     # ---------------------------------------------------------------- pieces
     @staticmethod
@@ -326,11 +358,12 @@ class _NativeEngine:
         torch.add(x0, m.pos_emb[:S], out=x0)  # positions 0..S-1 of the position table
         for l, lw in enumerate(m.layers):
             x, ln1, ln2 = b[f"x{l}"], b[f"ln1{l}"], b[f"ln2{l}"]
-            q, k, v, att, xmid = b[f"q{l}"], b[f"k{l}"], b[f"v{l}"], b[f"att{l}"], b[f"xmid{l}"]
+            qkv, att, xmid = b[f"qkv{l}"], b[f"att{l}"], b[f"xmid{l}"]
             self._ln(x, lw["ln1_g"], lw["ln1_b"], ln1, b[f"st1{l}"])
-            self._linear(ln1, lw["wq"], lw["bq"], q)
-            self._linear(ln1, lw["wk"], lw["bk"], k)
-            self._linear(ln1, lw["wv"], lw["bv"], v)
+            # Q, K, V in one GEMM ([S, 3d]), then split into three contiguous [S, d] tensors.
+            self._linear(ln1, self.wqkv[l], self.bqkv[l], b["wide"])
+            qkv.copy_(b["wide"].view(S, 3, -1).transpose(0, 1))
+            q, k, v = qkv[0], qkv[1], qkv[2]
             self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
             self._linear(att, lw["wo"], lw["bo"], b["tmp"])
             torch.add(x, b["tmp"], out=xmid)
@@ -383,7 +416,7 @@ class _NativeEngine:
     def _backward(self):
         torch = _torch()
         m, b = self.m, self.b
-        L = m.n_layers
+        L, S = m.n_layers, m.seq_len
         g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
         self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g)
         for l in reversed(range(L)):
@@ -403,15 +436,14 @@ class _NativeEngine:
             # attention: output projection, the fused attention backward, the Q/K/V projections
             self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"])
             self._bias_grad(g, lw["bo"])
-            self.ctx[l].backward_device_into(b[f"q{l}"], b[f"k{l}"], b[f"v{l}"], b["datt"], self.scale, True,
-                                             b["dq"], b["dk"], b["dv"])
-            ln1 = b[f"ln1{l}"]
-            self._linear_backward(ln1, lw["wq"], b["dq"], b["dln"])
-            self._linear_backward(ln1, lw["wk"], b["dk"], b["dln"], accumulate_dx=True)
-            self._linear_backward(ln1, lw["wv"], b["dv"], b["dln"], accumulate_dx=True)
-            self._bias_grad(b["dq"], lw["bq"])
-            self._bias_grad(b["dk"], lw["bk"])
-            self._bias_grad(b["dv"], lw["bv"])
+            qkv, dqkv = b[f"qkv{l}"], b["dqkv"]
+            self.ctx[l].backward_device_into(qkv[0], qkv[1], qkv[2], b["datt"], self.scale, True,
+                                             dqkv[0], dqkv[1], dqkv[2])
+            # dq | dk | dv side by side ([S, 3d]) for the fused projection's backward
+            wide = b["wide"]
+            wide.view(S, 3, -1).copy_(dqkv.transpose(0, 1))
+            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"])
+            self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
             self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other)
             torch.add(other, g, out=other)
