@@ -302,24 +302,34 @@ class _NativeEngine:
 
     # ---------------------------------------------------------------- pieces
     @staticmethod
-    def _linear(x, w, b, out):
-        """out = x W^T + b (static_gpt2.rs linear_into; hipBLASLt)."""
-        _torch().addmm(b, x, w.t(), out=out)
-
-    def _linear_backward(self, x, w, dy, dx, accumulate_dx=False, exact_dx=False):
-        """dx (=|+=) dy W; W's gradient = dy^T x and the bias's = column sums of dy, into the arena
-        gradient views (static_gpt2.rs linear_backward_into / _accumulate_into). exact_dx: dx on
-        the exact fp32 GEMM path (the faster one for that shape)."""
+    def _exact(flag=True):
+        """Switch the GEMMs that follow to hipBLASLt's exact fp32 path (flag) or back to the step's
+        setting (measured per call site: the fast path wins on the wide or deep products, the exact
+        one on the square 768 x 768 ones and on the products whose bias it fuses)."""
         torch = _torch()
-        if dx is not None:
-            fast = torch.backends.cuda.matmul.allow_tf32
-            torch.backends.cuda.matmul.allow_tf32 = fast and not exact_dx
-            if accumulate_dx:
-                dx.addmm_(dy, w)
-            else:
-                torch.mm(dy, w, out=dx)
-            torch.backends.cuda.matmul.allow_tf32 = fast
+        torch.backends.cuda.matmul.allow_tf32 = (not flag) and _NativeEngine._fast
+
+    def _linear(self, x, w, b, out, exact=True):
+        """out = x W^T + b (static_gpt2.rs linear_into; hipBLASLt). exact: one GEMM with the bias in
+        its epilogue on the exact fp32 path; otherwise the fast-path GEMM, then the bias added."""
+        torch = _torch()
+        if exact:
+            self._exact(True)
+            torch.addmm(b, x, w.t(), out=out)
+            self._exact(False)
+        else:
+            torch.mm(x, w.t(), out=out)
+            out.add_(b)
+
+    def _linear_backward(self, x, w, dy, dx, exact_dx=False, exact_dw=False):
+        """dx = dy W and W's gradient dy^T x, into the arena gradient view (static_gpt2.rs
+        linear_backward_into); exact_dx / exact_dw: that product on the exact fp32 GEMM path."""
+        torch = _torch()
+        self._exact(exact_dx)
+        torch.mm(dy, w, out=dx)
+        self._exact(exact_dw)
         torch.mm(dy.t(), x, out=w.grad)
+        self._exact(False)
 
     @staticmethod
     def _bias_grad(dy, b):
@@ -360,15 +370,16 @@ class _NativeEngine:
             x, ln1, ln2 = b[f"x{l}"], b[f"ln1{l}"], b[f"ln2{l}"]
             qkv, att, xmid = b[f"qkv{l}"], b[f"att{l}"], b[f"xmid{l}"]
             self._ln(x, lw["ln1_g"], lw["ln1_b"], ln1, b[f"st1{l}"])
-            # Q, K, V in one GEMM ([S, 3d]), then split into three contiguous [S, d] tensors.
-            self._linear(ln1, self.wqkv[l], self.bqkv[l], b["wide"])
-            qkv.copy_(b["wide"].view(S, 3, -1).transpose(0, 1))
+            # Q, K, V in one GEMM ([S, 3d]); the bias is added as the result is split into three
+            # contiguous [S, d] tensors.
+            torch.mm(ln1, self.wqkv[l].t(), out=b["wide"])
+            torch.add(b["wide"].view(S, 3, -1).transpose(0, 1), self.bqkv[l].view(3, 1, -1), out=qkv)
             q, k, v = qkv[0], qkv[1], qkv[2]
             self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
             self._linear(att, lw["wo"], lw["bo"], b["tmp"])
             torch.add(x, b["tmp"], out=xmid)
             self._ln(xmid, lw["ln2_g"], lw["ln2_b"], ln2, b[f"st2{l}"])
-            self._linear(ln2, lw["w1"], lw["b1"], b[f"h{l}"])
+            self._linear(ln2, lw["w1"], lw["b1"], b[f"h{l}"], exact=False)
             _ops._check(_ops.ops_lib().dfgpt2_gelu_forward(_ops._dev_ptr(b[f"h{l}"]), _ops._dev_ptr(b[f"a{l}"]),
                                                            b[f"a{l}"].numel(), _ops._stream_ptr()))
             self._linear(b[f"a{l}"], lw["w2"], lw["b2"], b["tmp"])
@@ -434,7 +445,7 @@ class _NativeEngine:
             torch.add(other, g, out=other)
             g, other = other, g
             # attention: output projection, the fused attention backward, the Q/K/V projections
-            self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"])
+            self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], exact_dw=True)
             self._bias_grad(g, lw["bo"])
             qkv, dqkv = b[f"qkv{l}"], b["dqkv"]
             self.ctx[l].backward_device_into(qkv[0], qkv[1], qkv[2], b["datt"], self.scale, True,
@@ -442,7 +453,7 @@ class _NativeEngine:
             # dq | dk | dv side by side ([S, 3d]) for the fused projection's backward
             wide = b["wide"]
             wide.view(S, 3, -1).copy_(dqkv.transpose(0, 1))
-            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"])
+            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], exact_dx=True)
             self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
             self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other)
@@ -456,10 +467,13 @@ class _NativeEngine:
     # (The parameters are autograd leaves for the comparator-facing API; the engine differentiates
     # by hand, so its torch calls run under no_grad. The GEMM precision setting is scoped to the
     # engine's own calls and restored afterwards.)
+    _fast = True  # the fast GEMM path is allowed in the running step (StaticGPT2.fast_gemm)
+
     def _run(self, fn):
         torch = _torch()
         prev = torch.backends.cuda.matmul.allow_tf32
-        torch.backends.cuda.matmul.allow_tf32 = bool(self.m.fast_gemm)
+        _NativeEngine._fast = bool(self.m.fast_gemm)
+        torch.backends.cuda.matmul.allow_tf32 = _NativeEngine._fast
         try:
             with torch.no_grad():
                 fn()
