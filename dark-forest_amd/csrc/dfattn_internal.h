@@ -14,6 +14,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -150,11 +151,18 @@ __device__ __forceinline__ float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// acc + sum of the 8 halves of h, accumulated in fp32 (v_dot2 with ones).
+// acc + the 8 halves of h, each widened to fp32 and added in order by
+// v_fma_mix_f32 (h * 1.0 + acc). A v_dot2 with ones would take two halves
+// per instruction, but it occupies the SIMD's matrix pipe (an MFMA of the
+// other wave on the SIMD stalls behind it); the mixed-precision fma issues
+// beside the MFMAs.
 __device__ __forceinline__ float sum8_f16(half8_t h, float acc) {
-  const half2_t one = {(half_t)1.f, (half_t)1.f};
+  const u32x4_t u = __builtin_bit_cast(u32x4_t, h);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(half2_t{h[2 * i], h[2 * i + 1]}, one, acc, false);
+  for (int i = 0; i < 4; ++i) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(u[i]));
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(u[i]));
+  }
   return acc;
 }
 
