@@ -36,23 +36,37 @@ __device__ __forceinline__ float hsum4(float4 v) { return (v.x + v.y) + (v.z + v
 // One wave per row, V float4 per lane held in registers (features <= 256 V,
 // features % 4 == 0, 16-byte aligned rows); four rows per 256-thread
 // workgroup. The mean, then the variance about it, as layernorm.cu:41-75.
+// With y: the row normalised is x + y (one fp32 add per value, a residual
+// connection), also stored to sum_out.
 template <int V>
-__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
-                                                         const float *__restrict__ beta, float *__restrict__ out,
-                                                         float *__restrict__ means, float *__restrict__ rstds,
-                                                         int batch, int features) {
+__global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float *__restrict__ x, const float *__restrict__ y,
+                                                         const float *__restrict__ gamma,
+                                                         const float *__restrict__ beta, float *__restrict__ sum_out,
+                                                         float *__restrict__ out, float *__restrict__ means,
+                                                         float *__restrict__ rstds, int batch, int features) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= batch) return;
   const int nv = features >> 2;
   const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * features);
+  const float4 *yr = reinterpret_cast<const float4 *>(y + (size_t)row * features);
   float4 v[V];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = lane + 64 * i;
     v[i] = c < nv ? xr[c] : splat4(0.f);
+    if (y != nullptr && c < nv) {
+      const float4 yv = yr[c];
+      v[i] = make_float4(v[i].x + yv.x, v[i].y + yv.y, v[i].z + yv.z, v[i].w + yv.w);
+    }
     s += hsum4(v[i]);
+  }
+  if (sum_out != nullptr) {
+    float4 *sr = reinterpret_cast<float4 *>(sum_out + (size_t)row * features);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (lane + 64 * i < nv) sr[lane + 64 * i] = v[i];
   }
   const float mean = wave_sum(s) / (float)features;
   float q = 0.f;
@@ -83,21 +97,23 @@ __global__ __launch_bounds__(256) void ln_fwd_vec_kernel(const float *__restrict
 
 // Any width and 4-byte alignment: one wave per row, three passes over the
 // row (it stays in the caches between them).
-__global__ __launch_bounds__(256) void ln_fwd_generic_kernel(const float *__restrict__ x,
+__global__ __launch_bounds__(256) void ln_fwd_generic_kernel(const float *__restrict__ x, const float *__restrict__ y,
                                                              const float *__restrict__ gamma,
-                                                             const float *__restrict__ beta, float *__restrict__ out,
-                                                             float *__restrict__ means, float *__restrict__ rstds,
-                                                             int batch, int features) {
+                                                             const float *__restrict__ beta, float *__restrict__ sum_out,
+                                                             float *__restrict__ out, float *__restrict__ means,
+                                                             float *__restrict__ rstds, int batch, int features) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= batch) return;
   const float *xr = x + (size_t)row * features;
+  const float *yr = y + (size_t)row * features;
+  auto val = [&](int c) { return y != nullptr ? xr[c] + yr[c] : xr[c]; };
   float s = 0.f;
-  for (int c = lane; c < features; c += 64) s += xr[c];
+  for (int c = lane; c < features; c += 64) s += val(c);
   const float mean = wave_sum(s) / (float)features;
   float q = 0.f;
   for (int c = lane; c < features; c += 64) {
-    const float d = xr[c] - mean;
+    const float d = val(c) - mean;
     q += d * d;
   }
   const float rstd = 1.f / sqrtf(wave_sum(q) / (float)features + kLnEps);
@@ -106,18 +122,24 @@ __global__ __launch_bounds__(256) void ln_fwd_generic_kernel(const float *__rest
     if (rstds) rstds[row] = rstd;
   }
   float *orow = out + (size_t)row * features;
-  for (int c = lane; c < features; c += 64)
-    orow[c] = (xr[c] - mean) * rstd * (gamma ? gamma[c] : 1.f) + (beta ? beta[c] : 0.f);
+  for (int c = lane; c < features; c += 64) {
+    const float v = val(c);
+    if (sum_out != nullptr) sum_out[(size_t)row * features + c] = v;
+    orow[c] = (v - mean) * rstd * (gamma ? gamma[c] : 1.f) + (beta ? beta[c] : 0.f);
+  }
 }
 
 // ------------------------------------------------------ LayerNorm backward, dx
 // grad_x = rstd / F * (F ds - sum(ds) - x_hat sum(ds x_hat)), ds = grad_out *
 // gamma (layernorm.cu:126-178). One wave per row, row in registers.
+// With residual: grad_x = that + residual (a residual connection's gradient
+// added in the same pass, one fp32 add per value).
 template <int V>
 __global__ __launch_bounds__(256) void ln_bwd_dx_vec_kernel(const float *__restrict__ dout, const float *__restrict__ x,
                                                             const float *__restrict__ gamma,
                                                             const float *__restrict__ means,
-                                                            const float *__restrict__ rstds, float *__restrict__ grad_x,
+                                                            const float *__restrict__ rstds,
+                                                            const float *__restrict__ residual, float *__restrict__ grad_x,
                                                             int batch, int features) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -144,12 +166,19 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_vec_kernel(const float *__restr
   const float sum_ds = wave_sum(sds), sum_dsx = wave_sum(sdsx);
   const float f = (float)features, k = rstd / f;
   float4 *gr = reinterpret_cast<float4 *>(grad_x + (size_t)row * features);
+  const float4 *rr = reinterpret_cast<const float4 *>(residual + (size_t)row * features);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int c = lane + 64 * i;
-    if (c < nv)
-      gr[c] = make_float4(k * (f * ds[i].x - sum_ds - xh[i].x * sum_dsx), k * (f * ds[i].y - sum_ds - xh[i].y * sum_dsx),
-                          k * (f * ds[i].z - sum_ds - xh[i].z * sum_dsx), k * (f * ds[i].w - sum_ds - xh[i].w * sum_dsx));
+    if (c < nv) {
+      float4 o = make_float4(k * (f * ds[i].x - sum_ds - xh[i].x * sum_dsx), k * (f * ds[i].y - sum_ds - xh[i].y * sum_dsx),
+                             k * (f * ds[i].z - sum_ds - xh[i].z * sum_dsx), k * (f * ds[i].w - sum_ds - xh[i].w * sum_dsx));
+      if (residual != nullptr) {
+        const float4 r = rr[c];
+        o = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+      }
+      gr[c] = o;
+    }
   }
 }
 
@@ -158,6 +187,7 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_generic_kernel(const float *__r
                                                                 const float *__restrict__ gamma,
                                                                 const float *__restrict__ means,
                                                                 const float *__restrict__ rstds,
+                                                                const float *__restrict__ residual,
                                                                 float *__restrict__ grad_x, int batch, int features) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -175,7 +205,8 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_generic_kernel(const float *__r
   float *gr = grad_x + (size_t)row * features;
   for (int c = lane; c < features; c += 64) {
     const float xh = (xr[c] - mean) * rstd, ds = dr[c] * (gamma ? gamma[c] : 1.f);
-    gr[c] = k * (f * ds - sum_ds - xh * sum_dsx);
+    const float o = k * (f * ds - sum_ds - xh * sum_dsx);
+    gr[c] = residual != nullptr ? o + residual[(size_t)row * features + c] : o;
   }
 }
 
@@ -320,6 +351,31 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float *__restrict__ go,
   }
 }
 
+// h = h + bias (bias broadcast over rows of `cols` values, written back: the
+// backward's GELU input) and out = gelu(h), in one pass over [rows, cols].
+// vec: cols % 4 == 0 and 16-byte aligned tensors.
+__global__ __launch_bounds__(256) void bias_gelu_kernel(float *__restrict__ h, const float *__restrict__ bias,
+                                                        float *__restrict__ out, size_t n, int cols, int vec) {
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  if (vec) {
+    const size_t n4 = n / 4;
+    const int c4 = cols / 4;
+    for (size_t i = tid; i < n4; i += stride) {
+      float4 v = reinterpret_cast<const float4 *>(h)[i];
+      const float4 b = reinterpret_cast<const float4 *>(bias)[i % c4];
+      v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+      reinterpret_cast<float4 *>(h)[i] = v;
+      reinterpret_cast<float4 *>(out)[i] = make_float4(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
+    }
+    return;
+  }
+  for (size_t i = tid; i < n; i += stride) {
+    const float v = h[i] + bias[i % cols];
+    h[i] = v;
+    out[i] = gelu_f(v);
+  }
+}
+
 // ------------------------------------------------------------------ AdamW
 // matmul.cu:285-339: m = b1 m + (1-b1) g, v = b2 v + (1-b2) g^2,
 // p = p (1 - lr wd) - lr m_hat / (sqrt(v_hat) + eps).
@@ -428,18 +484,26 @@ unsigned elementwise_blocks(size_t n) {
 }
 
 template <int V>
-void launch_ln_fwd_v(const float *x, const float *gamma, const float *beta, float *out, float *means, float *rstds,
-                     int batch, int features, hipStream_t stream) {
-  hipLaunchKernelGGL(ln_fwd_vec_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, x, gamma, beta, out, means,
-                     rstds, batch, features);
+void launch_ln_fwd_v(const float *x, const float *y, const float *gamma, const float *beta, float *sum_out, float *out,
+                     float *means, float *rstds, int batch, int features, hipStream_t stream) {
+  hipLaunchKernelGGL(ln_fwd_vec_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, x, y, gamma, beta, sum_out,
+                     out, means, rstds, batch, features);
 }
 
 template <int V>
 void launch_ln_dx_v(const float *dout, const float *x, const float *gamma, const float *means, const float *rstds,
-                    float *grad_x, int batch, int features, hipStream_t stream) {
+                    const float *residual, float *grad_x, int batch, int features, hipStream_t stream) {
   hipLaunchKernelGGL(ln_bwd_dx_vec_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, dout, x, gamma, means,
-                     rstds, grad_x, batch, features);
+                     rstds, residual, grad_x, batch, features);
 }
+
+// LayerNorm forward of x (+ y, stored to sum_out) on the register-resident
+// path when it applies, else the generic one.
+void ln_forward(const float *x, const float *y, const float *gamma, const float *beta, float *sum_out, float *out,
+                float *means, float *rstds, int b, int f, hipStream_t stream);
+// LayerNorm backward's grad_x (+ residual).
+void ln_backward_dx(const float *dout, const float *x, const float *gamma, const float *means, const float *rstds,
+                    const float *residual, float *grad_x, int b, int f, hipStream_t stream);
 
 // The register-resident row path: features % 4 == 0, at most 1024, 16-byte
 // aligned tensors.
@@ -448,6 +512,36 @@ bool ln_vec(uint32_t features, std::initializer_list<const void *> ptrs) {
   for (const void *p : ptrs)
     if (p != nullptr && !al(p, 16)) return false;
   return true;
+}
+
+void ln_forward(const float *x, const float *y, const float *gamma, const float *beta, float *sum_out, float *out,
+                float *means, float *rstds, int b, int f, hipStream_t stream) {
+  if (ln_vec((uint32_t)f, {x, y, out, sum_out, gamma, beta})) {
+    switch ((f / 4 + 63) / 64) {
+      case 1: launch_ln_fwd_v<1>(x, y, gamma, beta, sum_out, out, means, rstds, b, f, stream); break;
+      case 2: launch_ln_fwd_v<2>(x, y, gamma, beta, sum_out, out, means, rstds, b, f, stream); break;
+      case 3: launch_ln_fwd_v<3>(x, y, gamma, beta, sum_out, out, means, rstds, b, f, stream); break;
+      default: launch_ln_fwd_v<4>(x, y, gamma, beta, sum_out, out, means, rstds, b, f, stream); break;
+    }
+  } else {
+    hipLaunchKernelGGL(ln_fwd_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, x, y, gamma, beta, sum_out, out,
+                       means, rstds, b, f);
+  }
+}
+
+void ln_backward_dx(const float *dout, const float *x, const float *gamma, const float *means, const float *rstds,
+                    const float *residual, float *grad_x, int b, int f, hipStream_t stream) {
+  if (ln_vec((uint32_t)f, {dout, x, gamma, residual, grad_x})) {
+    switch ((f / 4 + 63) / 64) {
+      case 1: launch_ln_dx_v<1>(dout, x, gamma, means, rstds, residual, grad_x, b, f, stream); break;
+      case 2: launch_ln_dx_v<2>(dout, x, gamma, means, rstds, residual, grad_x, b, f, stream); break;
+      case 3: launch_ln_dx_v<3>(dout, x, gamma, means, rstds, residual, grad_x, b, f, stream); break;
+      default: launch_ln_dx_v<4>(dout, x, gamma, means, rstds, residual, grad_x, b, f, stream); break;
+    }
+  } else {
+    hipLaunchKernelGGL(ln_bwd_dx_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, dout, x, gamma, means, rstds,
+                       residual, grad_x, b, f);
+  }
 }
 
 template <bool LN>
@@ -473,18 +567,32 @@ extern "C" int dfgpt2_layernorm_forward(const float *x, const float *gamma, cons
   if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
   if (batch == 0) return DFATTN_OK;  // no rows: nothing to read or write
   if (int st = check_ptrs(fn, {x, out}, {gamma, beta, means, rstds}); st != DFATTN_OK) return st;
+  ln_forward(x, nullptr, gamma, beta, nullptr, out, means, rstds, (int)batch, (int)features, stream);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_add_layernorm_forward(const float *x, const float *y, const float *gamma, const float *beta,
+                                            float *sum_out, float *out, float *means, float *rstds, uint32_t batch,
+                                            uint32_t features, hipStream_t stream) {
+  const char *fn = "dfgpt2_add_layernorm_forward";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {x, y, sum_out, out}, {gamma, beta, means, rstds}); st != DFATTN_OK) return st;
+  ln_forward(x, y, gamma, beta, sum_out, out, means, rstds, (int)batch, (int)features, stream);
+  return launched(fn);
+}
+
+// grad_x, then the parameter gradients (added into grad_gamma / grad_beta, or
+// written when !accumulate) by the fixed-order column sums.
+static int ln_backward(const char *fn, const float *grad_out, const float *x, const float *gamma, const float *means,
+                       const float *rstds, const float *residual, float *grad_x, float *grad_gamma, float *grad_beta,
+                       int accumulate, uint32_t batch, uint32_t features, hipStream_t stream) {
   const int b = (int)batch, f = (int)features;
-  if (ln_vec(features, {x, out, gamma, beta})) {
-    switch ((f / 4 + 63) / 64) {
-      case 1: launch_ln_fwd_v<1>(x, gamma, beta, out, means, rstds, b, f, stream); break;
-      case 2: launch_ln_fwd_v<2>(x, gamma, beta, out, means, rstds, b, f, stream); break;
-      case 3: launch_ln_fwd_v<3>(x, gamma, beta, out, means, rstds, b, f, stream); break;
-      default: launch_ln_fwd_v<4>(x, gamma, beta, out, means, rstds, b, f, stream); break;
-    }
-  } else {
-    hipLaunchKernelGGL(ln_fwd_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, x, gamma, beta, out, means,
-                       rstds, b, f);
-  }
+  ln_backward_dx(grad_out, x, gamma, means, rstds, residual, grad_x, b, f, stream);
+  if (int st = launched(fn); st != DFATTN_OK) return st;
+  if (grad_gamma == nullptr && grad_beta == nullptr) return DFATTN_OK;
+  const bool vec = f % 4 == 0 && al(grad_out, 16) && al(x, 16);
+  launch_colsum<true>(grad_out, x, means, rstds, grad_gamma, grad_beta, b, f, accumulate, vec, stream);
   return launched(fn);
 }
 
@@ -496,23 +604,22 @@ extern "C" int dfgpt2_layernorm_backward(const float *grad_out, const float *x, 
   if (batch == 0) return DFATTN_OK;  // no rows: grad_x is empty and nothing is added
   if (int st = check_ptrs(fn, {grad_out, x, means, rstds, grad_x}, {gamma, grad_gamma, grad_beta}); st != DFATTN_OK)
     return st;
-  const int b = (int)batch, f = (int)features;
-  if (ln_vec(features, {grad_out, x, gamma, grad_x})) {
-    switch ((f / 4 + 63) / 64) {
-      case 1: launch_ln_dx_v<1>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
-      case 2: launch_ln_dx_v<2>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
-      case 3: launch_ln_dx_v<3>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
-      default: launch_ln_dx_v<4>(grad_out, x, gamma, means, rstds, grad_x, b, f, stream); break;
-    }
-  } else {
-    hipLaunchKernelGGL(ln_bwd_dx_generic_kernel, dim3((b + 3) / 4), dim3(256), 0, stream, grad_out, x, gamma, means,
-                       rstds, grad_x, b, f);
-  }
-  if (int st = launched(fn); st != DFATTN_OK) return st;
-  if (grad_gamma == nullptr && grad_beta == nullptr) return DFATTN_OK;
-  const bool vec = f % 4 == 0 && al(grad_out, 16) && al(x, 16);
-  launch_colsum<true>(grad_out, x, means, rstds, grad_gamma, grad_beta, b, f, 1, vec, stream);
-  return launched(fn);
+  return ln_backward(fn, grad_out, x, gamma, means, rstds, nullptr, grad_x, grad_gamma, grad_beta, 1, batch, features,
+                     stream);
+}
+
+extern "C" int dfgpt2_layernorm_backward_residual(const float *grad_out, const float *x, const float *gamma,
+                                                  const float *means, const float *rstds, const float *residual,
+                                                  float *grad_x, float *grad_gamma, float *grad_beta, uint32_t batch,
+                                                  uint32_t features, hipStream_t stream) {
+  const char *fn = "dfgpt2_layernorm_backward_residual";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {grad_out, x, means, rstds, grad_x}, {gamma, residual, grad_gamma, grad_beta});
+      st != DFATTN_OK)
+    return st;
+  return ln_backward(fn, grad_out, x, gamma, means, rstds, residual, grad_x, grad_gamma, grad_beta, 0, batch, features,
+                     stream);
 }
 
 extern "C" int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream) {
@@ -531,6 +638,19 @@ extern "C" int dfgpt2_gelu_backward(const float *grad_out, const float *x, float
   if (int st = check_ptrs(fn, {grad_out, x, grad_x}, {}); st != DFATTN_OK) return st;
   hipLaunchKernelGGL(gelu_kernel<true>, dim3(elementwise_blocks(n)), dim3(256), 0, stream, grad_out, x, grad_x, n,
                      (al(grad_out, 16) && al(x, 16) && al(grad_x, 16)) ? 1 : 0);
+  return launched(fn);
+}
+
+extern "C" int dfgpt2_bias_gelu_forward(float *h, const float *bias, float *out, uint32_t rows, uint32_t cols,
+                                        hipStream_t stream) {
+  const char *fn = "dfgpt2_bias_gelu_forward";
+  if (int st = check_dims(fn, rows, cols); st != DFATTN_OK) return st;
+  if (rows == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {h, bias, out}, {}); st != DFATTN_OK) return st;
+  const size_t n = (size_t)rows * cols;
+  const int vec = (cols % 4 == 0 && al(h, 16) && al(bias, 16) && al(out, 16)) ? 1 : 0;
+  hipLaunchKernelGGL(bias_gelu_kernel, dim3(elementwise_blocks(n)), dim3(256), 0, stream, h, bias, out, n, (int)cols,
+                     vec);
   return launched(fn);
 }
 

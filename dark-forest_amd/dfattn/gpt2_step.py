@@ -345,12 +345,10 @@ class _NativeEngine:
             _ops._dev_ptr(stats[1]), rows, f, _ops._stream_ptr()))
 
     @staticmethod
-    def _ln_backward(dy, x, g, b, stats, dx):
-        """dx overwritten; gamma's and beta's gradients added into their (zeroed) arena views."""
-        rows, f = x.shape
-        _ops._check(_ops.ops_lib().dfgpt2_layernorm_backward(
-            _ops._dev_ptr(dy), _ops._dev_ptr(x), _ops._dev_ptr(g), _ops._dev_ptr(stats[0]), _ops._dev_ptr(stats[1]),
-            _ops._dev_ptr(dx), _ops._dev_ptr(g.grad), _ops._dev_ptr(b.grad), rows, f, _ops._stream_ptr()))
+    def _ln_backward(dy, x, g, b, stats, dx, residual=None):
+        """dx = LayerNorm's input gradient (+ residual, a residual connection's gradient); gamma's
+        and beta's gradients written into their arena views."""
+        _ops.layer_norm_backward_residual_into(dy, x, g, stats, residual, dx, g.grad, b.grad)
 
     def _set_batch(self, tokens, targets):
         if tokens.shape[0] != self.m.seq_len or targets.shape[0] != self.m.seq_len:
@@ -360,16 +358,19 @@ class _NativeEngine:
 
     # ---------------------------------------------------------------- forward (static_gpt2.rs:1286-1373)
     def _forward(self):
+        """Each residual add runs inside the LayerNorm that follows it (x_mid and LayerNorm 2, then
+        x_in[l+1] and the next layer's LayerNorm 1 or the final one), and the first MLP bias inside
+        GELU; the values are those of the separate operations."""
         torch = _torch()
         m, b = self.m, self.b
-        S = m.seq_len
+        S, L = m.seq_len, m.n_layers
         x0 = b["x0"]
         _ops.embedding_forward(self.ids, m.tok_emb, x0)
         torch.add(x0, m.pos_emb[:S], out=x0)  # positions 0..S-1 of the position table
+        self._ln(x0, m.layers[0]["ln1_g"], m.layers[0]["ln1_b"], b["ln10"], b["st10"])
         for l, lw in enumerate(m.layers):
             x, ln1, ln2 = b[f"x{l}"], b[f"ln1{l}"], b[f"ln2{l}"]
             qkv, att, xmid = b[f"qkv{l}"], b[f"att{l}"], b[f"xmid{l}"]
-            self._ln(x, lw["ln1_g"], lw["ln1_b"], ln1, b[f"st1{l}"])
             # Q, K, V in one GEMM ([S, 3d]); the bias is added as the result is split into three
             # contiguous [S, d] tensors.
             torch.mm(ln1, self.wqkv[l].t(), out=b["wide"])
@@ -377,14 +378,18 @@ class _NativeEngine:
             q, k, v = qkv[0], qkv[1], qkv[2]
             self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
             self._linear(att, lw["wo"], lw["bo"], b["tmp"])
-            torch.add(x, b["tmp"], out=xmid)
-            self._ln(xmid, lw["ln2_g"], lw["ln2_b"], ln2, b[f"st2{l}"])
-            self._linear(ln2, lw["w1"], lw["b1"], b[f"h{l}"], exact=False)
-            _ops._check(_ops.ops_lib().dfgpt2_gelu_forward(_ops._dev_ptr(b[f"h{l}"]), _ops._dev_ptr(b[f"a{l}"]),
-                                                           b[f"a{l}"].numel(), _ops._stream_ptr()))
+            _ops.add_layer_norm_forward_into(x, b["tmp"], lw["ln2_g"], lw["ln2_b"], xmid, ln2, b[f"st2{l}"])
+            # h = ln2 W1^T on the fast GEMM path; the bias goes into h as GELU reads it
+            self._exact(False)
+            torch.mm(ln2, lw["w1"].t(), out=b[f"h{l}"])
+            _ops.bias_gelu_forward_into(b[f"h{l}"], lw["b1"], b[f"a{l}"])
             self._linear(b[f"a{l}"], lw["w2"], lw["b2"], b["tmp"])
-            torch.add(xmid, b["tmp"], out=b[f"x{l + 1}"])
-        self._ln(b[f"x{m.n_layers}"], m.ln_f_g, m.ln_f_b, b["lnf"], b["stf"])
+            if l + 1 < L:
+                nxt = m.layers[l + 1]
+                _ops.add_layer_norm_forward_into(xmid, b["tmp"], nxt["ln1_g"], nxt["ln1_b"], b[f"x{l + 1}"],
+                                                 b[f"ln1{l + 1}"], b[f"st1{l + 1}"])
+            else:
+                _ops.add_layer_norm_forward_into(xmid, b["tmp"], m.ln_f_g, m.ln_f_b, b[f"x{L}"], b["lnf"], b["stf"])
 
     # ---------------------------------------------------------------- loss (static_gpt2.rs:1386-1418)
     def _loss_and_head_backward(self):
@@ -441,8 +446,7 @@ class _NativeEngine:
             self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], exact_dx=True)
             self._bias_grad(b["dh"], lw["b1"])
             # d(x_mid) = g + LayerNorm 2's gradient
-            self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other)
-            torch.add(other, g, out=other)
+            self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other, residual=g)
             g, other = other, g
             # attention: output projection, the fused attention backward, the Q/K/V projections
             self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], exact_dw=True)
@@ -456,12 +460,17 @@ class _NativeEngine:
             self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], exact_dx=True)
             self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
-            self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other)
-            torch.add(other, g, out=other)
+            self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other, residual=g)
             g, other = other, g
         # embeddings (static_gpt2.rs:1559-1574): the token rows, and positions 0..S-1
         _ops.embedding_backward(self.ids, g, m.tok_emb.grad)
         _ops.embedding_backward(self.pos, g, m.pos_emb.grad)
+
+    def _zero_accumulated_grads(self):
+        """Only the embedding gradients are accumulated (the embedding backward adds into them);
+        every other gradient of the arena is written whole by the step."""
+        self.m.tok_emb.grad.zero_()
+        self.m.pos_emb.grad.zero_()
 
     # ---------------------------------------------------------------- public
     # (The parameters are autograd leaves for the comparator-facing API; the engine differentiates
@@ -489,9 +498,10 @@ class _NativeEngine:
         return self.b["loss"][0]
 
     def step(self, tokens, targets):
-        """static_gpt2.rs:1375-1696: forward, chunked loss, backward, AdamW; returns the device loss."""
+        """static_gpt2.rs:1375-1696: forward, chunked loss, backward, AdamW over the whole parameter
+        arena in one launch; returns the device loss."""
         def run():
-            self.m.opt.zero_grad()
+            self._zero_accumulated_grads()
             self._set_batch(tokens, targets)
             self._forward()
             self._loss_and_head_backward()

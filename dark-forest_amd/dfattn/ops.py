@@ -45,6 +45,9 @@ SYMBOLS = {
     "dfgpt2_sum": (_I, [_P, _U32, _P, _I, _P]),
     "dfgpt2_embedding_forward": (_I, [_P] * 3 + [_U32, _U32, _U32, _P]),
     "dfgpt2_embedding_backward": (_I, [_P] * 3 + [_U32, _U32, _U32, _P]),
+    "dfgpt2_add_layernorm_forward": (_I, [_P] * 8 + [_U32, _U32, _P]),
+    "dfgpt2_layernorm_backward_residual": (_I, [_P] * 9 + [_U32, _U32, _P]),
+    "dfgpt2_bias_gelu_forward": (_I, [_P] * 3 + [_U32, _U32, _P]),
 }
 
 _typed = None
@@ -90,6 +93,31 @@ def layer_norm_backward(grad_out, x, gamma, means, rstds):
                                                _dev_ptr(rstds), _dev_ptr(grad_x), _dev_ptr(pg[0]), _dev_ptr(pg[1]),
                                                rows, f, _stream_ptr()))
     return grad_x, pg[0], pg[1]
+
+
+def add_layer_norm_forward_into(x, y, gamma, beta, sum_out, out, stats):
+    """dfgpt2_add_layernorm_forward: sum_out = x + y, out = LayerNorm(sum_out) with eps 1e-5;
+    stats[0], stats[1] receive the rows' means and reciprocal standard deviations."""
+    rows, f = _rows_cols(x)
+    _check(ops_lib().dfgpt2_add_layernorm_forward(_dev_ptr(x), _dev_ptr(y), _dev_ptr(gamma), _dev_ptr(beta),
+                                                  _dev_ptr(sum_out), _dev_ptr(out), _dev_ptr(stats[0]),
+                                                  _dev_ptr(stats[1]), rows, f, _stream_ptr()))
+
+
+def layer_norm_backward_residual_into(grad_out, x, gamma, stats, residual, grad_x, grad_gamma, grad_beta):
+    """dfgpt2_layernorm_backward_residual: grad_x = LayerNorm backward (+ residual unless None);
+    grad_gamma and grad_beta are overwritten."""
+    rows, f = _rows_cols(x)
+    res = _dev_ptr(residual) if residual is not None else None
+    _check(ops_lib().dfgpt2_layernorm_backward_residual(
+        _dev_ptr(grad_out), _dev_ptr(x), _dev_ptr(gamma), _dev_ptr(stats[0]), _dev_ptr(stats[1]), res,
+        _dev_ptr(grad_x), _dev_ptr(grad_gamma), _dev_ptr(grad_beta), rows, f, _stream_ptr()))
+
+
+def bias_gelu_forward_into(h, bias, out):
+    """dfgpt2_bias_gelu_forward: h += bias (per column, in place), out = gelu(h)."""
+    rows, cols = _rows_cols(h)
+    _check(ops_lib().dfgpt2_bias_gelu_forward(_dev_ptr(h), _dev_ptr(bias), _dev_ptr(out), rows, cols, _stream_ptr()))
 
 
 def bias_grad(grad_out):
@@ -243,3 +271,4 @@ class ArenaAdamW:
         _check(ops_lib().dfgpt2_adamw_update(_dev_ptr(a.p), _dev_ptr(a.m), _dev_ptr(a.v), _dev_ptr(a.g), a.numel,
                                              g["lr"], b1, b2, g["eps"], g["weight_decay"], _dev_ptr(a.step),
                                              _stream_ptr()))
+

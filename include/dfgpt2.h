@@ -89,6 +89,25 @@ int dfgpt2_embedding_forward(const uint32_t *indices, const float *table, float 
 int dfgpt2_embedding_backward(const uint32_t *indices, const float *grad_out, float *grad_table, uint32_t n_rows,
                               uint32_t dim, uint32_t rows_in_table, hipStream_t stream);
 
+/* Fused forms the engine's step uses; no reference counterparts (the reference's step runs these
+ * as separate launches: a residual add, then LayerNorm, static_gpt2.rs:1341-1350, 1360 with
+ * 1315 / 1364; LayerNorm's backward, then the residual gradient added, 1474-1486, 1543-1555; the
+ * linear layer with its bias, then GELU, 1353-1355).
+ * dfgpt2_add_layernorm_forward: sum_out = x + y (one fp32 add per value), out = LayerNorm(sum_out)
+ * with means / rstds as dfgpt2_layernorm_forward.                                           */
+int dfgpt2_add_layernorm_forward(const float *x, const float *y, const float *gamma, const float *beta,
+                                 float *sum_out, float *out, float *means, float *rstds, uint32_t batch,
+                                 uint32_t features, hipStream_t stream);
+/* grad_x = LayerNorm backward of grad_out (+ residual when not NULL); grad_gamma and grad_beta
+ * (either may be NULL) are WRITTEN, not added into, so the caller need not zero them.      */
+int dfgpt2_layernorm_backward_residual(const float *grad_out, const float *x, const float *gamma,
+                                       const float *means, const float *rstds, const float *residual,
+                                       float *grad_x, float *grad_gamma, float *grad_beta, uint32_t batch,
+                                       uint32_t features, hipStream_t stream);
+/* h[r, c] += bias[c] in place (the GELU input the backward needs), out = gelu(h); [rows, cols]. */
+int dfgpt2_bias_gelu_forward(float *h, const float *bias, float *out, uint32_t rows, uint32_t cols,
+                             hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

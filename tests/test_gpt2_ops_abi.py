@@ -65,6 +65,19 @@ ODD = ctypes.c_void_p(0x1002)
     ("dfgpt2_embedding_forward", (None, None, None, 0, 8, 10, None), OK),
     ("dfgpt2_embedding_backward", (BUF, BUF, ODD, 4, 8, 10, None), ERR_MISALIGNED),
     ("dfgpt2_embedding_backward", (BUF, BUF, BUF, 2**31, 8, 10, None), ERR_OVERFLOW),
+    ("dfgpt2_add_layernorm_forward", (BUF, None, None, None, BUF, BUF, None, None, 4, 8, None), ERR_NULL),
+    ("dfgpt2_add_layernorm_forward", (BUF, BUF, None, None, ODD, BUF, None, None, 4, 8, None), ERR_MISALIGNED),
+    ("dfgpt2_add_layernorm_forward", (BUF, BUF, None, None, BUF, BUF, None, None, 4, 0, None), ERR_SHAPE),
+    ("dfgpt2_add_layernorm_forward", (None,) * 8 + (0, 8, None), OK),
+    ("dfgpt2_layernorm_backward_residual", (BUF, BUF, None, BUF, BUF, None, None, None, None, 4, 8, None),
+     ERR_NULL),
+    ("dfgpt2_layernorm_backward_residual", (BUF, BUF, None, BUF, BUF, ODD, BUF, None, None, 4, 8, None),
+     ERR_MISALIGNED),
+    ("dfgpt2_layernorm_backward_residual", (None,) * 9 + (0, 8, None), OK),
+    ("dfgpt2_bias_gelu_forward", (BUF, None, BUF, 4, 8, None), ERR_NULL),
+    ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 4, 0, None), ERR_SHAPE),
+    ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 2**31, 8, None), ERR_OVERFLOW),
+    ("dfgpt2_bias_gelu_forward", (None, None, None, 0, 8, None), OK),
 ])
 def test_argument_errors_are_caught_on_the_host(fn, args, status):
     ops.ops_lib().dfattn_clear_error()

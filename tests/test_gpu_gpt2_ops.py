@@ -281,3 +281,70 @@ def test_embedding_forward_and_backward_match_torch(device):
     ops.ops_lib().launch_embedding_backward(P(ids), P(gy), P(gt3), seq, dim)
     dfattn.darkforest_sync()
     assert torch.equal(out3, out) and torch.equal(gt3, gt)
+
+
+@pytest.mark.parametrize("rows,f", LN_SHAPES)
+def test_add_layernorm_is_the_add_then_the_layernorm(device, rows, f):
+    """dfgpt2_add_layernorm_forward: sum_out is x + y bit for bit and out is the LayerNorm of it
+    bit for bit (the same kernel as dfgpt2_layernorm_forward); out also against torch."""
+    import torch
+
+    say(f"add+layernorm rows={rows} f={f}")
+    g = torch.Generator(device="cpu").manual_seed(rows * 7 + f)
+    x = (torch.randn(rows, f, generator=g) * 2).to(device)
+    y = (torch.randn(rows, f, generator=g) + 0.25).to(device)
+    gamma, beta = torch.randn(f, generator=g).to(device), torch.randn(f, generator=g).to(device)
+    s, out = torch.empty_like(x), torch.empty_like(x)
+    stats = torch.empty((2, rows), device=device)
+    ops.add_layer_norm_forward_into(x, y, gamma, beta, s, out, stats)
+    want_out, want_m, want_r = ops.layer_norm_forward(x + y, gamma, beta)
+    torch.cuda.synchronize()
+    assert torch.equal(s, x + y)
+    assert torch.equal(out, want_out) and torch.equal(stats[0], want_m) and torch.equal(stats[1], want_r)
+    ref = torch.nn.functional.layer_norm(x + y, (f,), gamma, beta, 1e-5)
+    close(out, ref, 1e-5, 1e-5, "add+layernorm vs torch")
+
+
+@pytest.mark.parametrize("rows,f", LN_SHAPES)
+def test_layernorm_backward_residual_adds_and_overwrites(device, rows, f):
+    """dfgpt2_layernorm_backward_residual: grad_x is dfgpt2_layernorm_backward's plus the residual
+    (one fp32 add), the parameter gradients are written over whatever their buffers held."""
+    import torch
+
+    say(f"layernorm backward + residual rows={rows} f={f}")
+    g = torch.Generator(device="cpu").manual_seed(rows * 5 + f)
+    x, dy = torch.randn(rows, f, generator=g).to(device), torch.randn(rows, f, generator=g).to(device)
+    res = torch.randn(rows, f, generator=g).to(device)
+    gamma, beta = torch.randn(f, generator=g).to(device), torch.randn(f, generator=g).to(device)
+    _, m, r = ops.layer_norm_forward(x, gamma, beta)
+    gx0, gg0, gb0 = ops.layer_norm_backward(dy, x, gamma, m, r)
+    gx = torch.empty_like(x)
+    gg, gb = torch.full((f,), 7.0, device=device), torch.full((f,), -3.0, device=device)
+    stats = torch.stack([m, r])
+    ops.layer_norm_backward_residual_into(dy, x, gamma, stats, res, gx, gg, gb)
+    torch.cuda.synchronize()
+    assert torch.equal(gx, gx0 + res)
+    assert torch.equal(gg, gg0) and torch.equal(gb, gb0)
+    # without a residual: grad_x alone
+    ops.layer_norm_backward_residual_into(dy, x, gamma, stats, None, gx, gg, gb)
+    torch.cuda.synchronize()
+    assert torch.equal(gx, gx0)
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 3072), (7, 13), (5, 8)])
+def test_bias_gelu_is_the_bias_add_then_gelu(device, rows, cols):
+    """dfgpt2_bias_gelu_forward: h becomes h + bias (per column) bit for bit, out = gelu of it bit for
+    bit (dfgpt2_gelu_forward's function); also against torch's tanh GELU."""
+    import torch
+
+    say(f"bias+gelu rows={rows} cols={cols}")
+    h = torch.randn(rows, cols, device=device) * 3
+    b = torch.randn(cols, device=device)
+    want_h = h + b
+    want = ops.gelu_forward(want_h)
+    out = torch.empty_like(h)
+    ops.bias_gelu_forward_into(h, b, out)
+    torch.cuda.synchronize()
+    assert torch.equal(h, want_h) and torch.equal(out, want)
+    close(out, torch.nn.functional.gelu(want_h, approximate="tanh"), 1e-5, 1e-6, "bias+gelu vs torch")
+
