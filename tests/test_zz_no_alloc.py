@@ -57,8 +57,13 @@ def test_noalloc_matches_dfattn_bwd_on_two_calls(device):
         for name, a, b in zip(("dq", "dk", "dv"), got, ref):
             assert torch.equal(a, b), f"S={seq_len} {name}: differs from dfattn_bwd"
         if seq_len <= 1000:
+            # S = 1000 is not a BASELINE shape: the parity suite's bar for fp16-operand shapes,
+            # max-abs <= 2e-3 * max(1, max|ref|) and relative L2 <= 1e-3
             want = O.backward(x["q"], x["k"], x["v"], x["do"], 12, 0.125, True, threads=8)
             for name, a, w in zip(("dq", "dk", "dv"), got, want):
-                err = float(np.max(np.abs(a.cpu().numpy().astype(np.float64) - w)))
-                say(f"S={seq_len} {name} max-abs vs oracle {err:.2e}")
-                assert err <= 2e-3
+                d = a.cpu().numpy().astype(np.float64) - w
+                err = float(np.max(np.abs(d)))
+                rel = float(np.linalg.norm(d) / np.linalg.norm(w))
+                bar = 2e-3 * max(1.0, float(np.max(np.abs(w))))
+                say(f"S={seq_len} {name} vs oracle: max-abs {err:.3e} (bar {bar:.2e}), rel-L2 {rel:.2e}")
+                assert err <= bar and rel <= 1e-3
