@@ -513,6 +513,8 @@ def main():
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
+    ap.add_argument("--flush-mib", type=int, default=1024,
+                    help="cold-cache steps: MiB written before each of up to 20 event-timed steps (0 = skip)")
     ap.add_argument("--sclk", type=int, default=1,
                     help="1: sample the shader clock with rocm-smi while the step runs (0 under a profiler, whose "
                          "preloaded library must not see bench.py start another program)")
@@ -629,6 +631,27 @@ def main():
     torch.cuda.synchronize()
     step_ev_ms = sorted(e[0].elapsed_time(e[1]) for e in events)
     log(f"fwd {fwd_ms:.4f} ms, bwd preprocess {pre_ms:.4f} ms, bwd main {main_ms:.4f} ms, wall/step {ms_per_step:.4f} ms")
+    # Cold caches: before each of these steps a plain write of `flush_mib`
+    # MiB evicts the step's tensors from the L2s and the 256 MB Infinity Cache; events around the
+    # step alone.
+    flushed = None
+    if args.flush_mib > 0:
+        junk = torch.empty(args.flush_mib << 18, dtype=torch.float32, device=q.device)
+        cold = []
+        for i in range(min(args.steps, 20)):
+            junk.fill_(float(i))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            step()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            cold.append(e0.elapsed_time(e1))
+        cold.sort()
+        flushed = {"flush_mib": args.flush_mib, "steps": len(cold), "median_ms": round(cold[len(cold) // 2], 5),
+                   "min_ms": round(cold[0], 5),
+                   "tflops_at_median": round(FLOP_STEP / (cold[len(cold) // 2] * 1e-3) / 1e12, 2)}
+        del junk
+        log(f"cold-cache step (after a {args.flush_mib} MiB write): median {flushed['median_ms']:.4f} ms")
 
     kernels = {
         "fwd_d64_kernel": (fwd_ms, FLOP_FWD),
@@ -669,6 +692,7 @@ def main():
         "step_event_ms_min": round(step_ev_ms[0], 5),
         "step_event_ms_p90": round(step_ev_ms[min(len(step_ev_ms) - 1, (9 * len(step_ev_ms)) // 10)], 5),
         "roofline": roofline,
+        "cold_cache_step": flushed,
         "gpt2_step_ms": None,
     }
     # The shader clock the kernels ran at (rocm-smi, sampled while the same step runs back to back
@@ -681,7 +705,8 @@ def main():
         roofline["peak_at_sclk"] = round(peak_sclk, 1)
         roofline["frac_at_sclk"] = round(roofline["achieved"] / peak_sclk, 4)
     result["notes"] = ("inputs L2/MALL-warm: the step's ~150 MB of tensors stay resident between steps "
-                       "(the 256 MB Infinity Cache); no flush buffer between steps. The device runs the step "
+                       "(the 256 MB Infinity Cache); no flush buffer between the timed steps (cold_cache_step "
+                       "times steps that each follow a flush write). The device runs the step "
                        "back to back for `preheat.seconds` before the warmup steps, so the timed steps run at "
                        "the working clock rather than during the ramp from idle")
     if args.decode:
