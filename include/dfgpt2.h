@@ -94,17 +94,20 @@ int dfgpt2_embedding_backward(const uint32_t *indices, const float *grad_out, fl
  * 1315 / 1364; LayerNorm's backward, then the residual gradient added, 1474-1486, 1543-1555; the
  * linear layer with its bias, then GELU, 1353-1355).
  * dfgpt2_add_layernorm_forward: sum_out = x + y (one fp32 add per value), out = LayerNorm(sum_out)
- * with means / rstds as dfgpt2_layernorm_forward.                                           */
+ * with means / rstds as dfgpt2_layernorm_forward. sum_out and out must not overlap x, y or each
+ * other.                                                                                      */
 int dfgpt2_add_layernorm_forward(const float *x, const float *y, const float *gamma, const float *beta,
                                  float *sum_out, float *out, float *means, float *rstds, uint32_t batch,
                                  uint32_t features, hipStream_t stream);
 /* grad_x = LayerNorm backward of grad_out (+ residual when not NULL); grad_gamma and grad_beta
- * (either may be NULL) are WRITTEN, not added into, so the caller need not zero them.      */
+ * (either may be NULL) are WRITTEN, not added into, so the caller need not zero them. grad_x
+ * must not overlap grad_out, x or residual.                                                  */
 int dfgpt2_layernorm_backward_residual(const float *grad_out, const float *x, const float *gamma,
                                        const float *means, const float *rstds, const float *residual,
                                        float *grad_x, float *grad_gamma, float *grad_beta, uint32_t batch,
                                        uint32_t features, hipStream_t stream);
-/* h[r, c] += bias[c] in place (the GELU input the backward needs), out = gelu(h); [rows, cols]. */
+/* h[r, c] += bias[c] in place (the GELU input the backward needs), out = gelu(h); [rows, cols];
+ * out must not overlap h.                                                                      */
 int dfgpt2_bias_gelu_forward(float *h, const float *bias, float *out, uint32_t rows, uint32_t cols,
                              hipStream_t stream);
 
