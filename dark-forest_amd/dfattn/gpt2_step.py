@@ -25,13 +25,15 @@ construction (`_NativeEngine`), the weights, gradients and AdamW moments are one
 (`ops.ParamArena`), and every kernel but the GEMMs is this library's (include/dfgpt2.h and the
 attention contexts): embedding gather and gradient, LayerNorm, tanh GELU, the bias gradients, the
 chunked fused cross-entropy and one AdamW launch over the whole arena, all fp32; the GEMMs are
-hipBLASLt fp32. attention="sdpa", and any model on the CPU, is the reference's own parity comparator
+hipBLASLt / rocBLAS fp32, with per-shape solutions TunableOp measured (GEMM_SOLUTIONS).
+attention="sdpa", and any model on the CPU, is the reference's own parity comparator
 instead (scripts/verify_loss_parity.py:58): the same model in plain PyTorch operators with torch's
 scaled_dot_product_attention and torch's AdamW, differentiated by autograd.
 """
 from __future__ import annotations
 
 import math
+import os
 import struct
 import time
 
@@ -50,6 +52,57 @@ def _f32(x):
     return struct.unpack("<f", struct.pack("<f", x))[0]
 
 
+# GEMM solutions PyTorch's TunableOp measured fastest for the engine's GEMM shapes (GPT-2 small, S =
+# 1024) on MI355X with this image's PyTorch, HIP, hipBLASLt and rocBLAS (written by tune_gemms). Each
+# call keeps its math mode: the fast fp32 call sites choose among hipBLASLt's fast fp32 solutions,
+# the exact ones among exact fp32 solutions (rocBLAS or hipBLASLt). The file's validators make
+# TunableOp ignore it under other library versions or GPUs, shapes it does not list keep the
+# library's default solution, and no tuning runs inside a step.
+GEMM_SOLUTIONS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_solutions_gpt2_mi355x.csv")
+_solutions_loaded = False
+
+
+def _load_gemm_solutions():
+    global _solutions_loaded
+    if _solutions_loaded:
+        return
+    _solutions_loaded = True
+    tun = _torch().cuda.tunable
+    if not tun.is_enabled():
+        # TunableOp writes its table to its file at exit once enabled: not into the caller's cwd.
+        tun.set_filename(os.devnull)
+    if os.path.exists(GEMM_SOLUTIONS):
+        tun.read_file(GEMM_SOLUTIONS)
+
+
+def tune_gemms(path=GEMM_SOLUTIONS, seq_len=1024, steps=2, seed=0):
+    """Measure the engine's GEMM shapes with TunableOp (GPT-2 small at seq_len) and write the
+    fastest solution per shape, with the library versions as validators, to `path` (the format
+    TunableOp reads). Takes a few seconds on the GPU."""
+    torch = _torch()
+    tun = torch.cuda.tunable
+    model = StaticGPT2(seq_len=seq_len, seed=seed, tuned_gemms=False)
+    tokens, targets = synthetic_batch(model.vocab_size, seq_len, 1, model.device)
+    prev = tun.is_enabled(), tun.tuning_is_enabled()
+    tun.enable(True)
+    tun.tuning_enable(True)
+    try:
+        for _ in range(steps):
+            model._engine.step(tokens, targets, tuned=False)
+        torch.cuda.synchronize()
+        validators = tun.get_validators()
+        results = tun.get_results()
+    finally:
+        tun.tuning_enable(prev[1])
+        tun.enable(prev[0])
+    with open(path, "w") as f:
+        for key, value in validators:
+            f.write(f"Validator,{key},{value}\n")
+        for op_sig, param_sig, solution, ms in results:
+            f.write(f"{op_sig},{param_sig},{solution},{ms}\n")
+    return len(results)
+
+
 # A layer's parameters in parameters() (and arena) order.
 _PARAM_ORDER = ("ln1_g", "ln1_b", "wq", "wk", "wv", "bq", "bk", "bv", "wo", "bo", "ln2_g", "ln2_b", "w1", "b1", "w2",
                 "b2")
@@ -59,7 +112,7 @@ class StaticGPT2:
     """GPT-2 with the reference engine's architecture, init and optimizer."""
 
     def __init__(self, vocab_size=50257, d_model=768, n_heads=12, n_layers=12, d_ff=3072, seq_len=1024, lr=3e-4,
-                 seed=0, device="cuda", attention="dfattn", capturable=False, fast_gemm=True):
+                 seed=0, device="cuda", attention="dfattn", capturable=False, fast_gemm=True, tuned_gemms=True):
         torch = _torch()
         if d_model % n_heads:
             raise ValueError("d_model must be divisible by n_heads")
@@ -108,6 +161,9 @@ class StaticGPT2:
         # error ~5e-6 on these shapes against 1e-6 for the exact path, far inside the TF32 the
         # reference's cuBLAS GEMMs use (lib.rs:45-48), and up to 2.3x faster on the lm_head GEMM.
         self.fast_gemm = fast_gemm
+        # tuned_gemms: the engine's GEMMs take the solutions in GEMM_SOLUTIONS (TunableOp, no tuning
+        # at run time); the comparator's are untouched.
+        self.tuned_gemms = tuned_gemms
         if self.native:
             arena = _ops.ParamArena(self.parameters(), self.device)
             self._rebind(arena.adopt(self.parameters()))
@@ -478,15 +534,24 @@ class _NativeEngine:
     # engine's own calls and restored afterwards.)
     _fast = True  # the fast GEMM path is allowed in the running step (StaticGPT2.fast_gemm)
 
-    def _run(self, fn):
+    def _run(self, fn, tuned=True):
         torch = _torch()
+        tun = torch.cuda.tunable
         prev = torch.backends.cuda.matmul.allow_tf32
+        prev_tun = tun.is_enabled(), tun.tuning_is_enabled()
         _NativeEngine._fast = bool(self.m.fast_gemm)
         torch.backends.cuda.matmul.allow_tf32 = _NativeEngine._fast
+        if tuned and self.m.tuned_gemms:
+            _load_gemm_solutions()
+            tun.enable(True)
+            tun.tuning_enable(False)
         try:
             with torch.no_grad():
                 fn()
         finally:
+            if tuned and self.m.tuned_gemms:
+                tun.tuning_enable(prev_tun[1])
+                tun.enable(prev_tun[0])
             torch.backends.cuda.matmul.allow_tf32 = prev
 
     def forward_loss(self, tokens, targets):
@@ -497,9 +562,10 @@ class _NativeEngine:
         self._run(run)
         return self.b["loss"][0]
 
-    def step(self, tokens, targets):
+    def step(self, tokens, targets, tuned=True):
         """static_gpt2.rs:1375-1696: forward, chunked loss, backward, AdamW over the whole parameter
-        arena in one launch; returns the device loss."""
+        arena in one launch; returns the device loss. tuned=False: TunableOp's state is left as
+        the caller set it (tune_gemms measures through it)."""
         def run():
             self._zero_accumulated_grads()
             self._set_batch(tokens, targets)
@@ -507,7 +573,7 @@ class _NativeEngine:
             self._loss_and_head_backward()
             self._backward()
             self.m.opt.step()
-        self._run(run)
+        self._run(run, tuned=tuned)
         return self.b["loss"][0]
 
 

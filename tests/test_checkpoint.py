@@ -171,3 +171,4 @@ def test_safetensors_import_errors(tmp_path):
     save_file({"wte.weight": np.zeros((2, 2), np.float16)}, str(tmp_path / "f16"))
     with pytest.raises(ValueError, match="only F32"):
         C.load_gpt2_safetensors(tiny(), tmp_path / "f16")
+

@@ -58,6 +58,20 @@ def test_full_gpt2_small_initial_loss_and_descent(device):
     assert math.isfinite(last) and last < first
 
 
+def test_tuned_gemm_solutions_match_the_default_ones(device):
+    """GPT-2 small with the tuned GEMM solutions (GEMM_SOLUTIONS: the S=1024 shapes) against the same
+    model on the libraries' default solutions: the same losses over two steps within the parity bar
+    (the solutions differ only in blocking and summation order)."""
+    say("GPT-2 small: tuned GEMM solutions against the default ones")
+    tokens, targets = synthetic_batch(50257, 1024, 2, device)
+    a = StaticGPT2(seed=0)
+    b = StaticGPT2(seed=0, tuned_gemms=False)
+    for step in range(2):
+        la, lb = float(a.step(tokens, targets)), float(b.step(tokens, targets))
+        say(f"step {step}: tuned {la:.6f} default {lb:.6f}")
+        assert abs(la - lb) < 1e-3
+
+
 def test_checkpoints_carry_the_gpu_model(device, tmp_path):
     """The reference's binary checkpoint resumes the GPU run; its safetensors export loads the same
     weights into a CPU PyTorch twin (SDPA attention), whose loss then matches within the parity bar."""
