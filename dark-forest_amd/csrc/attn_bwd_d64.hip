@@ -348,23 +348,39 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // units (an exact power-of-two product). Every wave sees every block's scale
   // in the same order, so partners end in the same units.
   int sig_cur = __float_as_int(1.f);
+  // When every block the workgroup walks has one scale (the usual case:
+  // blocks of similar magnitude share it), the accumulators start in that
+  // unit and no block's scale is read back. (Zero accumulators in another
+  // unit equal zero in this one, so the results are those of the per-block
+  // checks.)
+  bool sig_uniform;
+  {
+    const float *sg = a.sigma + (size_t)head * a.n_blocks;
+    const int s0 = __builtin_amdgcn_readfirstlane(__float_as_int(sg[min(first_qb, a.n_blocks - 1)]));
+    bool differs = false;
+    for (int b = first_qb + lane; b < n_qblocks; b += 64) differs |= __float_as_int(sg[b]) != s0;
+    sig_uniform = !__any(differs);
+    if (sig_uniform) sig_cur = s0;
+  }
 
   // One block. `masked`: the block may hold the causal diagonal, so rows
   // below this wave's keys are masked and a wave whose rows are all below
   // its keys skips the block.
   auto compute = [&](int i, int st, bool masked) {
-    const int sig_b = __builtin_amdgcn_readfirstlane(
-        __float_as_int(*reinterpret_cast<const float *>(stage_base(st) + kStageSigma)));
-    if (sig_b != sig_cur) {
-      const float ratio = __int_as_float(sig_b) / __int_as_float(sig_cur);
+    if (!sig_uniform) {
+      const int sig_b = __builtin_amdgcn_readfirstlane(
+          __float_as_int(*reinterpret_cast<const float *>(stage_base(st) + kStageSigma)));
+      if (sig_b != sig_cur) {
+        const float ratio = __int_as_float(sig_b) / __int_as_float(sig_cur);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        dk[0][r] *= ratio;
-        dk[1][r] *= ratio;
-        dv[0][r] *= ratio;
-        dv[1][r] *= ratio;
+        for (int r = 0; r < 16; ++r) {
+          dk[0][r] *= ratio;
+          dk[1][r] *= ratio;
+          dv[0][r] *= ratio;
+          dv[1][r] *= ratio;
+        }
+        sig_cur = sig_b;
       }
-      sig_cur = sig_b;
     }
     const int q0 = (first_qb + i) * kQBlock + qh * 32;  // this wave's first query row
     if (masked && q0 + 31 < key0) return;

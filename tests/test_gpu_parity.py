@@ -172,6 +172,21 @@ def test_small_gradient_magnitudes(device):
         assert er <= REL_L2 and ea <= bar, f"{name}: {ea:.2e} (bar {bar:.2e}) {er:.2e}"
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_dO_blocks_of_different_magnitudes(device, causal):
+    """Each 64-row block of dO gets its own power-of-two scale in the backward. Blocks scaled by 1/16,
+    1 and 16 in turn get three different scales, so the dK/dV accumulators change units between
+    blocks (a wrong unit would be off by 16x or more). Both the one-call backward and the timed
+    training sequence are compared with the oracle."""
+    say(f"dO blocks scaled 1/16, 1, 16 in turn, H=2 S=1000 causal={causal}")
+    x = O.seeded_inputs(1000, 2, 64, 7100 + int(causal))
+    mags = np.array([1 / 16, 1.0, 16.0], np.float32)
+    x["do"] = x["do"] * mags[(np.arange(1000) // 64) % 3][:, None]
+    want = oracle_fwd_bwd(x, 2, 0.125, causal)
+    compare(f"one call c={int(causal)}", run_fwd_bwd(x, 2, 0.125, causal, device), want, scaled=True)
+    compare(f"training pair c={int(causal)}", run_training_pair(x, 2, 0.125, causal, device), want, scaled=True)
+
+
 # ---------------------------------------------------------------- known-answer tests of the reference
 def test_reference_kat_forward(device):
     say("reference KAT forward (lib.rs:2605-2628), single-head launcher")
