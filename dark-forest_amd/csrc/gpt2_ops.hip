@@ -391,6 +391,15 @@ __device__ __forceinline__ void adamw1(float &p, float &m, float &v, float g, fl
 // (every load of both issued before the arithmetic), the n % 4 tail by the
 // first workgroup; otherwise one value per thread.
 constexpr int kAdamGroups = 2;
+// Each value is read and written once per step: streaming (nontemporal)
+// accesses, which do not keep the 2 GB the update moves in the caches.
+typedef float stream4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 stream_load4(const float *base, size_t i) {
+  return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const stream4_t *>(base) + i));
+}
+__device__ __forceinline__ void stream_store4(float *base, size_t i, float4 x) {
+  __builtin_nontemporal_store(__builtin_bit_cast(stream4_t, x), reinterpret_cast<stream4_t *>(base) + i);
+}
 __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float *__restrict__ m,
                                                     float *__restrict__ v, const float *__restrict__ g, size_t n,
                                                     float lr, float b1, float b2, float eps, float wd, float bc1,
@@ -413,10 +422,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float
   for (int k = 0; k < kAdamGroups; ++k) {
     const size_t i = base + 256 * k;
     if (i < n4) {
-      pp[k] = reinterpret_cast<const float4 *>(p)[i];
-      mm[k] = reinterpret_cast<const float4 *>(m)[i];
-      vv[k] = reinterpret_cast<const float4 *>(v)[i];
-      gg[k] = reinterpret_cast<const float4 *>(g)[i];
+      pp[k] = stream_load4(p, i);
+      mm[k] = stream_load4(m, i);
+      vv[k] = stream_load4(v, i);
+      gg[k] = stream_load4(g, i);
     }
   }
 #pragma unroll
@@ -427,9 +436,9 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ p, float
       adamw1(pp[k].y, mm[k].y, vv[k].y, gg[k].y, lr, b1, b2, eps, decay, bc1, bc2);
       adamw1(pp[k].z, mm[k].z, vv[k].z, gg[k].z, lr, b1, b2, eps, decay, bc1, bc2);
       adamw1(pp[k].w, mm[k].w, vv[k].w, gg[k].w, lr, b1, b2, eps, decay, bc1, bc2);
-      reinterpret_cast<float4 *>(p)[i] = pp[k];
-      reinterpret_cast<float4 *>(m)[i] = mm[k];
-      reinterpret_cast<float4 *>(v)[i] = vv[k];
+      stream_store4(p, i, pp[k]);
+      stream_store4(m, i, mm[k]);
+      stream_store4(v, i, vv[k]);
     }
   }
   if (blockIdx.x == 0) {
