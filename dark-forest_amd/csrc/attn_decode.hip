@@ -55,14 +55,22 @@ __device__ __forceinline__ float bf16_bits_to_float(unsigned short b) {
 
 // 4 consecutive values of a cache row: the raw bits (fp32: the floats; bf16:
 // four bf16 in the low 8 bytes), loaded without conversion so that every
-// load of a group is issued before the first wait, and widened later.
+// load of a group is issued before the first wait, and widened later. A
+// call reads each cache row once, and a long cache is larger than the
+// caches: the loads are nontemporal (streaming), which measured 10-11 %
+// faster at 131072 rows than cached loads.
+typedef unsigned raw2_t __attribute__((ext_vector_type(2)));
+typedef unsigned raw4_t __attribute__((ext_vector_type(4)));
 template <bool BF16>
 __device__ __forceinline__ uint4 load4_raw(const void *base, size_t elem) {
   if constexpr (BF16) {
-    const uint2 u = *reinterpret_cast<const uint2 *>(reinterpret_cast<const unsigned short *>(base) + elem);
+    const raw2_t u = __builtin_nontemporal_load(
+        reinterpret_cast<const raw2_t *>(reinterpret_cast<const unsigned short *>(base) + elem));
     return make_uint4(u.x, u.y, 0u, 0u);
   } else {
-    return *reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(base) + elem);
+    const raw4_t u =
+        __builtin_nontemporal_load(reinterpret_cast<const raw4_t *>(reinterpret_cast<const float *>(base) + elem));
+    return make_uint4(u.x, u.y, u.z, u.w);
   }
 }
 template <bool BF16>
