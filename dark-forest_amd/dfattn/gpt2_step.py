@@ -285,6 +285,7 @@ class _NativeEngine:
     def __init__(self, m: StaticGPT2):
         torch = _torch()
         self.m = m
+        self.exact_sites = dict(self.EXACT_SITES)
         S, d, F, V, L, H = m.seq_len, m.d_model, m.d_ff, m.vocab_size, m.n_layers, m.n_heads
         self.chunk = min(S, 512)  # static_gpt2.rs:423
         dev = m.device
@@ -357,6 +358,14 @@ class _NativeEngine:
         w.grad = torch.as_strided(first.grad, shape, first.grad.stride())
         return w
 
+    # Per GEMM call site: the exact fp32 path (True) or the fast one, whichever measured faster at
+    # that site with the tuned solutions (whole replayed steps: qkv_fwd exact is 0.12 ms slower,
+    # qkv_dw and wo_dx exact no faster). *_fwd: the forward product (o and fc2 with the bias in the
+    # GEMM's epilogue); *_dx / *_dw: the input and weight gradients.
+    EXACT_SITES = {"qkv_fwd": False, "o_fwd": True, "fc1_fwd": False, "fc2_fwd": True,
+                   "fc2_dx": False, "fc2_dw": False, "fc1_dx": True, "fc1_dw": False,
+                   "wo_dx": False, "wo_dw": True, "qkv_dx": True, "qkv_dw": False}
+
     # ---------------------------------------------------------------- pieces
     @staticmethod
     def _exact(flag=True):
@@ -419,7 +428,7 @@ class _NativeEngine:
         x_in[l+1] and the next layer's LayerNorm 1 or the final one), and the first MLP bias inside
         GELU; the values are those of the separate operations."""
         torch = _torch()
-        m, b = self.m, self.b
+        m, b, ex = self.m, self.b, self.exact_sites
         S, L = m.seq_len, m.n_layers
         x0 = b["x0"]
         _ops.embedding_forward(self.ids, m.tok_emb, x0)
@@ -430,17 +439,19 @@ class _NativeEngine:
             qkv, att, xmid = b[f"qkv{l}"], b[f"att{l}"], b[f"xmid{l}"]
             # Q, K, V in one GEMM ([S, 3d]); the bias is added as the result is split into three
             # contiguous [S, d] tensors.
+            self._exact(ex["qkv_fwd"])
             torch.mm(ln1, self.wqkv[l].t(), out=b["wide"])
             torch.add(b["wide"].view(S, 3, -1).transpose(0, 1), self.bqkv[l].view(3, 1, -1), out=qkv)
             q, k, v = qkv[0], qkv[1], qkv[2]
             self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
-            self._linear(att, lw["wo"], lw["bo"], b["tmp"])
+            self._linear(att, lw["wo"], lw["bo"], b["tmp"], ex["o_fwd"])
             _ops.add_layer_norm_forward_into(x, b["tmp"], lw["ln2_g"], lw["ln2_b"], xmid, ln2, b[f"st2{l}"])
-            # h = ln2 W1^T on the fast GEMM path; the bias goes into h as GELU reads it
-            self._exact(False)
+            # h = ln2 W1^T; the bias goes into h as GELU reads it
+            self._exact(ex["fc1_fwd"])
             torch.mm(ln2, lw["w1"].t(), out=b[f"h{l}"])
+            self._exact(False)
             _ops.bias_gelu_forward_into(b[f"h{l}"], lw["b1"], b[f"a{l}"])
-            self._linear(b[f"a{l}"], lw["w2"], lw["b2"], b["tmp"])
+            self._linear(b[f"a{l}"], lw["w2"], lw["b2"], b["tmp"], ex["fc2_fwd"])
             if l + 1 < L:
                 nxt = m.layers[l + 1]
                 _ops.add_layer_norm_forward_into(xmid, b["tmp"], nxt["ln1_g"], nxt["ln1_b"], b[f"x{l + 1}"],
@@ -488,25 +499,25 @@ class _NativeEngine:
     # ---------------------------------------------------------------- backward (static_gpt2.rs:1424-1575)
     def _backward(self):
         torch = _torch()
-        m, b = self.m, self.b
+        m, b, ex = self.m, self.b, self.exact_sites
         L, S = m.n_layers, m.seq_len
         g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
         self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g)
         for l in reversed(range(L)):
             lw = m.layers[l]
             # MLP: g is d(x_in[l+1]) = d(mlp out) = d(x_mid) through the residual
-            self._linear_backward(b[f"a{l}"], lw["w2"], g, b["da"])
+            self._linear_backward(b[f"a{l}"], lw["w2"], g, b["da"], ex["fc2_dx"], ex["fc2_dw"])
             self._bias_grad(g, lw["b2"])
             _ops._check(_ops.ops_lib().dfgpt2_gelu_backward(_ops._dev_ptr(b["da"]), _ops._dev_ptr(b[f"h{l}"]),
                                                             _ops._dev_ptr(b["dh"]), b["dh"].numel(),
                                                             _ops._stream_ptr()))
-            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], exact_dx=True)
+            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], ex["fc1_dx"], ex["fc1_dw"])
             self._bias_grad(b["dh"], lw["b1"])
             # d(x_mid) = g + LayerNorm 2's gradient
             self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other, residual=g)
             g, other = other, g
             # attention: output projection, the fused attention backward, the Q/K/V projections
-            self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], exact_dw=True)
+            self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], ex["wo_dx"], ex["wo_dw"])
             self._bias_grad(g, lw["bo"])
             qkv, dqkv = b[f"qkv{l}"], b["dqkv"]
             self.ctx[l].backward_device_into(qkv[0], qkv[1], qkv[2], b["datt"], self.scale, True,
@@ -514,7 +525,7 @@ class _NativeEngine:
             # dq | dk | dv side by side ([S, 3d]) for the fused projection's backward
             wide = b["wide"]
             wide.view(S, 3, -1).copy_(dqkv.transpose(0, 1))
-            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], exact_dx=True)
+            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], ex["qkv_dx"], ex["qkv_dw"])
             self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
             self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other, residual=g)
