@@ -173,6 +173,33 @@ def test_small_gradient_magnitudes(device):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+def test_forward_reference_point_moves(device, causal):
+    """The forward keeps a row's softmax reference point until a score exceeds it by more than 8 (in
+    log2 units) and then rescales O, l and the next tile's issued scores. Here the keys' dimension
+    0 climbs a staircase (1 more every 128 keys) against q_0 = 96, so every row's scores rise by 12
+    log2 units at each step and its reference point moves several times. With scale = ln2/8 the
+    kernel's c2 = scale*log2(e) is 2^-3 exactly, and Q, K on a 1/16 grid are exact in fp16, so the
+    scores carry no operand rounding and the bar is the usual one. (The large factor sits in Q:
+    in K it would multiply dS, whose rows sum to zero, inside dQ = dS K and amplify dS's fp16
+    rounding by that factor.)"""
+    say(f"staircase keys (reference point moves), H=3 S=1000 causal={causal}")
+    rng = np.random.default_rng(7200 + int(causal))
+    S, H, D = 1000, 3, 64
+    grid = lambda a: (np.round(a * 16) / 16).astype(np.float32)  # noqa: E731
+    q = grid(rng.standard_normal((S, H, D)))
+    k = grid(rng.standard_normal((S, H, D)))
+    q[:, :, 0] = 96.0
+    k[:, :, 0] = (np.arange(S) // 128)[:, None]
+    x = {"q": q.reshape(S, H * D), "k": k.reshape(S, H * D),
+         "v": rng.standard_normal((S, H * D)).astype(np.float32),
+         "do": rng.standard_normal((S, H * D)).astype(np.float32)}
+    scale = float(np.log(2.0) / 8)
+    want = oracle_fwd_bwd(x, H, scale, causal)
+    compare(f"staircase c={int(causal)}", run_fwd_bwd(x, H, scale, causal, device), want, scaled=True)
+    compare(f"staircase pair c={int(causal)}", run_training_pair(x, H, scale, causal, device), want, scaled=True)
+
+
+@pytest.mark.parametrize("causal", [True, False])
 def test_dO_blocks_of_different_magnitudes(device, causal):
     """Each 64-row block of dO gets its own power-of-two scale in the backward. Blocks scaled by 1/16,
     1 and 16 in turn get three different scales, so the dK/dV accumulators change units between
