@@ -143,6 +143,21 @@ def test_ragged_seq_len(device, seq_len, causal):
             oracle_fwd_bwd(x, 3, 0.125, causal), scaled=True)
 
 
+@pytest.mark.parametrize("seq_len,n_heads", [(2049, 5), (3071, 2), (4097, 3)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_long_ragged_seq_len(device, seq_len, n_heads, causal):
+    """Lengths just past and short of the 64-key and 128-row tiles at the scale of C2, odd head
+    counts: the masked tails, the pipelined loops' remainders and the backward's last pair, through
+    both the one-call path and the timed training sequence."""
+    say(f"long ragged S={seq_len} H={n_heads} causal={causal}")
+    x = O.seeded_inputs(seq_len, n_heads, 64, 8000 + seq_len + n_heads)
+    want = oracle_fwd_bwd(x, n_heads, 0.125, causal)
+    compare(f"S={seq_len} H={n_heads} c={int(causal)}", run_fwd_bwd(x, n_heads, 0.125, causal, device), want,
+            scaled=True)
+    compare(f"pair S={seq_len} H={n_heads} c={int(causal)}", run_training_pair(x, n_heads, 0.125, causal, device),
+            want, scaled=True)
+
+
 @pytest.mark.parametrize("d_head,n_heads", [(3, 2), (32, 4), (100, 2), (128, 2)])
 def test_generic_head_dims(device, d_head, n_heads):
     say(f"generic D={d_head} H={n_heads} S=77")
