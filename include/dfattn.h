@@ -184,7 +184,12 @@ void darkforest_sync(void);
 /* ---- Group 2: fast path -------------------------------------------------
  * `stream` is a hipStream_t passed as an opaque pointer (NULL = the null
  * stream). All validation happens on the host before any HIP call; on error
- * nothing is launched and a negative dfattn_status is returned.            */
+ * nothing is launched and a negative dfattn_status is returned.
+ * d_head = 64 runs on fp16 MFMA operands: scale*log2(e)*q, k and v are
+ * rounded to fp16, so their magnitudes must stay below 65504 (fp16's largest
+ * finite value); beyond it they overflow and the outputs are not finite.
+ * d_out needs no such bound (each 64-row block is scaled by a power of two
+ * before rounding). Other d_head values run in fp32 like the reference.   */
 
 /* Forward: O [S, H*D] and lse [H, S] (lse may be NULL to skip it).
  * No allocation: only the caller's Q, K, V, O and lse are touched.
