@@ -38,6 +38,7 @@ struct dfattn_context {
   const float *last_out = nullptr;
   float last_scale = 0.f;
   uint32_t last_causal = 0;
+  uint32_t last_qkv_stride = 0;  // 0: contiguous
   // Opt-in: the backward may reuse the last forward (caller guarantees that
   // q, k, v and that forward's out are unchanged and still allocated).
   bool reuse_forward = false;
@@ -79,14 +80,25 @@ int check_dims(uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   return DFATTN_OK;
 }
 
+// A row stride of exactly n_heads * d_head is the contiguous layout: 0, so that
+// a forward and a backward that name it differently still match for reuse.
+uint32_t packed_or(const dfattn_context *c, uint32_t stride) {
+  return stride == c->n_heads * c->d_head ? 0 : stride;
+}
+
 // The forward also leaves the backward's fp16 copies of Q, K and V in the
 // context's workspace (dfattn_fwd_train), which the backward on the same
-// q, k, v then reuses.
+// q, k, v then reuses. qkv_stride: the row stride of q, k, v (0: contiguous).
 int run_forward(dfattn_context *c, const float *q, const float *k, const float *v, float scale,
-                uint32_t causal, float *out, void *stream) {
-  const int st = dfattn_fwd_train(q, k, v, out, c->lse, c->workspace, c->workspace_bytes, c->n_heads,
-                                  c->seq_len, c->d_head, scale, causal, stream);
+                uint32_t causal, float *out, uint32_t qkv_stride, void *stream) {
+  const int st = qkv_stride == 0
+                     ? dfattn_fwd_train(q, k, v, out, c->lse, c->workspace, c->workspace_bytes, c->n_heads,
+                                        c->seq_len, c->d_head, scale, causal, stream)
+                     : dfattn_fwd_train_strided(q, k, v, out, c->lse, c->workspace, c->workspace_bytes,
+                                                c->n_heads, c->seq_len, c->d_head, scale, causal, qkv_stride,
+                                                stream);
   if (st == DFATTN_OK) {
+    c->last_qkv_stride = qkv_stride;
     c->last_q = q;
     c->last_k = k;
     c->last_v = v;
@@ -97,21 +109,28 @@ int run_forward(dfattn_context *c, const float *q, const float *k, const float *
   return st;
 }
 
+// qkv_stride / grad_stride: the row strides of q, k, v and of d_q, d_k, d_v
+// (0: contiguous).
 int run_backward(dfattn_context *c, const float *q, const float *k, const float *v,
                  const float *d_out, float scale, uint32_t causal, float *d_q, float *d_k,
-                 float *d_v, void *stream) {
+                 float *d_v, uint32_t qkv_stride, uint32_t grad_stride, void *stream) {
   const float *o = c->last_out;
   if (!(c->reuse_forward && q == c->last_q && k == c->last_k && v == c->last_v && o != nullptr &&
-        scale == c->last_scale && causal == c->last_causal)) {
+        scale == c->last_scale && causal == c->last_causal && qkv_stride == c->last_qkv_stride)) {
     int st = ensure(&c->own_out, c->elems);
     if (st != DFATTN_OK) return st;
-    st = run_forward(c, q, k, v, scale, causal, c->own_out, stream);
+    st = run_forward(c, q, k, v, scale, causal, c->own_out, qkv_stride, stream);
     if (st != DFATTN_OK) return st;
     o = c->own_out;
   }
+  // The forward left the fp16 copies: preprocess reads only o, d_out and
+  // lse, so q, k, v pass as they are whatever their stride.
   const int st = dfattn_bwd_preprocess(q, k, v, o, d_out, c->lse, c->workspace, c->workspace_bytes,
                                        c->n_heads, c->seq_len, c->d_head, scale, DFATTN_BWD_QKV_SAVED, stream);
   if (st != DFATTN_OK) return st;
+  if (grad_stride != 0)
+    return dfattn_bwd_main_strided(c->lse, d_q, d_k, d_v, c->workspace, c->workspace_bytes, c->n_heads,
+                                   c->seq_len, c->d_head, scale, causal, grad_stride, stream);
   return dfattn_bwd_main(q, k, v, o, d_out, c->lse, d_q, d_k, d_v, c->workspace, c->workspace_bytes,
                          c->n_heads, c->seq_len, c->d_head, scale, causal, stream);
 }
@@ -191,7 +210,17 @@ int dfattn_context_forward_device_into(dfattn_context *c, const float *q, const 
   if (c == nullptr) return fail(DFATTN_ERR_NULL_POINTER, "null attention context");
   if (out_elems != c->elems) return fail(DFATTN_ERR_SHAPE, "attention output shape mismatch");
   std::lock_guard<std::mutex> lock(c->mu);
-  return run_forward(c, q, k, v, scale, causal, out, stream);
+  return run_forward(c, q, k, v, scale, causal, out, 0, stream);
+}
+
+int dfattn_context_forward_device_into_strided(dfattn_context *c, const float *q, const float *k,
+                                               const float *v, float scale, uint32_t causal, float *out,
+                                               size_t out_elems, uint32_t qkv_row_stride, void *stream) {
+  if (c == nullptr) return fail(DFATTN_ERR_NULL_POINTER, "null attention context");
+  if (out_elems != c->elems) return fail(DFATTN_ERR_SHAPE, "attention output shape mismatch");
+  if (qkv_row_stride == 0) return fail(DFATTN_ERR_SHAPE, "row stride must be >= n_heads*d_head");
+  std::lock_guard<std::mutex> lock(c->mu);
+  return run_forward(c, q, k, v, scale, causal, out, packed_or(c, qkv_row_stride), stream);
 }
 
 int dfattn_context_backward_device_into(dfattn_context *c, const float *q, const float *k,
@@ -201,7 +230,21 @@ int dfattn_context_backward_device_into(dfattn_context *c, const float *q, const
   if (c == nullptr) return fail(DFATTN_ERR_NULL_POINTER, "null attention context");
   if (grad_elems != c->elems) return fail(DFATTN_ERR_SHAPE, "attention backward output shape mismatch");
   std::lock_guard<std::mutex> lock(c->mu);
-  return run_backward(c, q, k, v, d_out, scale, causal, d_q, d_k, d_v, stream);
+  return run_backward(c, q, k, v, d_out, scale, causal, d_q, d_k, d_v, 0, 0, stream);
+}
+
+int dfattn_context_backward_device_into_strided(dfattn_context *c, const float *q, const float *k,
+                                                const float *v, const float *d_out, float scale,
+                                                uint32_t causal, float *d_q, float *d_k, float *d_v,
+                                                size_t grad_elems, uint32_t qkv_row_stride,
+                                                uint32_t grad_row_stride, void *stream) {
+  if (c == nullptr) return fail(DFATTN_ERR_NULL_POINTER, "null attention context");
+  if (grad_elems != c->elems) return fail(DFATTN_ERR_SHAPE, "attention backward output shape mismatch");
+  if (qkv_row_stride == 0 || grad_row_stride == 0)
+    return fail(DFATTN_ERR_SHAPE, "row strides must be >= n_heads*d_head");
+  std::lock_guard<std::mutex> lock(c->mu);
+  return run_backward(c, q, k, v, d_out, scale, causal, d_q, d_k, d_v, packed_or(c, qkv_row_stride),
+                      packed_or(c, grad_row_stride), stream);
 }
 
 // lib.rs:2295-2326: upload q, k, v into context buffers, run the single-head

@@ -127,13 +127,14 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const float *__restrict__ O, const float *__restrict__ dO, const float *__restrict__ lse,
     float *__restrict__ sigma_out, float *__restrict__ lse2n, float *__restrict__ deltan,
     half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
-    int H, int S, float c2, int convert_qkv) {
+    int H, int S, float c2, int convert_qkv, int ldi) {
   __shared__ float wmax[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
   const int row = blockIdx.x * kPreRows + (tid >> 2);
   const bool ok = row < S;
   const size_t src = ok ? (size_t)row * H * kD + (size_t)head * kD + (tid & 3) * 16 : 0;
+  const size_t src_in = ok ? (size_t)row * ldi + (size_t)head * kD + (tid & 3) * 16 : 0;  // Q, K, V
   const size_t dst = ((size_t)head * S + row) * kD + (tid & 3) * 16;
   const size_t r = (size_t)head * S + row;
   // Every load first.
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
 #pragma unroll
     for (int t = 0; t < 3; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src + 4 * i, ok);
+      for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src_in + 4 * i, ok);
   }
   const float l = ok ? lse[r] : 0.f;
   float mx = 0.f;
@@ -216,6 +217,7 @@ struct BwdArgs {
   const float *lse2n, *deltan, *sigma;
   float *dQ, *dK, *dV;
   int H, S, causal, n_blocks;
+  int ldg;  // row stride of dQ, dK and dV in floats
   float scale;
 };
 
@@ -281,7 +283,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   const int c = lane & 31, hh = lane >> 5;
   const int kg = wave & 3, qh = wave >> 2;
   const int S = a.S;
-  const int ld = a.H * kD, hoff = head * kD;
+  const int ld = a.ldg, hoff = head * kD;
   const int key0 = kv_blk0 + kg * 32;  // this wave's first key
   const int key = key0 + c;
 
@@ -531,7 +533,7 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   const int c = lane & 31, hh = lane >> 5;
   const int qg = wave & 3, kh = wave >> 2;
   const int S = a.S;
-  const size_t ld = (size_t)a.H * kD, hoff = (size_t)head * kD;
+  const size_t ld = (size_t)a.ldg, hoff = (size_t)head * kD;
   const int q_w0 = q_blk0 + qg * 32;
   const int query = q_w0 + c;
   const bool q_ok = query < S;
@@ -830,7 +832,7 @@ void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, 
 
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
                               const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
-                              float scale, hipStream_t stream, bool qkv_saved) {
+                              float scale, hipStream_t stream, bool qkv_saved, int ldi) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   hipLaunchKernelGGL(bwd_prep_kernel, dim3(pre_blocks(seq_len), n_heads), dim3(256), 0, stream, q, k, v, o, d_o,
@@ -838,12 +840,13 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
                      reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
                      reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, scale * kLog2e,
-                     qkv_saved ? 0 : 1);
+                     qkv_saved ? 0 : 1, ldi > 0 ? ldi : n_heads * kD);
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
-                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream) {
+                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream,
+                               int ldg) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   const unsigned char *ws = static_cast<const unsigned char *>(workspace);
   BwdArgs a;
@@ -862,6 +865,7 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
   a.causal = causal ? 1 : 0;
   a.n_blocks = pre_blocks(seq_len);
   a.scale = scale;
+  a.ldg = ldg > 0 ? ldg : n_heads * kD;
   Sched sched;
   sched.n_qblocks = (seq_len + kQBlock - 1) / kQBlock;
   sched.n_qtiles = (seq_len + kQueriesPerWg - 1) / kQueriesPerWg;

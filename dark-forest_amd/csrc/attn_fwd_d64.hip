@@ -78,7 +78,7 @@ __device__ __forceinline__ half4_t lds_tr4(const unsigned char *p) {
 __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     float *__restrict__ O, float *__restrict__ LSE, int H, int S, float qscale, int causal,
-    int n_qtiles, half_t *__restrict__ Q16, half_t *__restrict__ K16, half_t *__restrict__ V16) {
+    int n_qtiles, half_t *__restrict__ Q16, half_t *__restrict__ K16, half_t *__restrict__ V16, int ldi) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -89,7 +89,9 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   const int head = blockIdx.x % H;
   // Longest query tiles first under causal masking (they see the most keys).
   const int qtile = causal ? (n_qtiles - 1 - (int)(blockIdx.x / H)) : (int)(blockIdx.x / H);
-  const int ld = H * kD;
+  const int ld = H * kD;  // row stride of O
+  // (ldi: the row stride of Q, K and V, which may be column blocks of a wider
+  // tensor such as a fused [S, 3 H D] projection.)
   const int hoff = head * kD;
 
   const int q_blk0 = qtile * kBM;
@@ -116,12 +118,12 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   const bool save = Q16 != nullptr;
   {
     const unsigned rows = (unsigned)max(0, min(S - q_blk0, kBM));
-    const size_t base = (size_t)min(q_blk0, S) * ld;
-    const auto rq = buffer_rsrc(Q + base, rows * (unsigned)ld * 4);
+    const size_t base = (size_t)min(q_blk0, S) * ldi;
+    const auto rq = buffer_rsrc(Q + base, rows * (unsigned)ldi * 4);
 #pragma unroll
     for (int k = 0; k < kQF4; ++k) {
       const int idx = tid + k * kThreads;
-      qraw[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4, 0, 0));
+      qraw[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rq, ((idx >> 4) * ldi + hoff + (idx & 15) * 4) * 4, 0, 0));
     }
   }
 
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       for (int hf = 0; hf < 2; ++hf)
         voff[j][db][hf] = 2 * tile_tr4_off(16 * (2 * kh + j) + 8 * hf + 4 * hh, 32 * db + 16 * ((lane >> 4) & 1), lane);
   soff = 2 * tile_off(tid >> 3, (tid & 7) * 8);
-  goff = ((tid >> 3) * ld + hoff + (tid & 7) * 8) * 4;
+  goff = ((tid >> 3) * ldi + hoff + (tid & 7) * 8) * 4;
 
   // LDS stages: K tile t in K stage t % 4, V tile t in V stage t % 4.
   auto kstage = [&](int t) { return lds_raw + (t & (kStages - 1)) * kTileBytes; };
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
   auto load_rows = [&](const float *X, int t, float4 (&xr)[kF4]) {
     const int kv0 = t * kBN;
     const int rows = uniform_clamp0<kBN>(S - kv0);  // (n_heads <= 65535: 64 rows span < 2^30 bytes)
-    const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ld, (unsigned)rows * (unsigned)(ld * 4));
+    const auto rx = buffer_rsrc(X + (size_t)min(kv0, S) * ldi, (unsigned)rows * (unsigned)(ldi * 4));
 #pragma unroll
     for (int i = 0; i < kF4; ++i)
       xr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, goff + 16 * i, 0, 0));
@@ -522,14 +524,14 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       // its own query tile from the inputs.
       const int r0 = q_blk0;
       const unsigned rows = (unsigned)max(0, min(S - r0, kBM));
-      const size_t base = (size_t)min(r0, S) * ld;
-      const auto rk = buffer_rsrc(K + base, rows * (unsigned)ld * 4);
-      const auto rv = buffer_rsrc(V + base, rows * (unsigned)ld * 4);
+      const size_t base = (size_t)min(r0, S) * ldi;
+      const auto rk = buffer_rsrc(K + base, rows * (unsigned)ldi * 4);
+      const auto rv = buffer_rsrc(V + base, rows * (unsigned)ldi * 4);
       float4 kx[kQF4], vx[kQF4];
 #pragma unroll
       for (int k = 0; k < kQF4; ++k) {
         const int idx = tid + k * kThreads;
-        const int off = ((idx >> 4) * ld + hoff + (idx & 15) * 4) * 4;
+        const int off = ((idx >> 4) * ldi + hoff + (idx & 15) * 4) * 4;
         kx[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
         vx[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
       }
@@ -593,13 +595,14 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
 
 hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float *o, float *lse,
                           int n_heads, int seq_len, float scale, bool causal,
-                          hipStream_t stream, void *bwd_workspace) {
+                          hipStream_t stream, void *bwd_workspace, int ldi) {
   const int n_qtiles = (seq_len + kBM - 1) / kBM;
   const dim3 grid((unsigned)(n_qtiles * n_heads));
   half_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
   if (bwd_workspace != nullptr) bwd_ws_qkv_copies(bwd_workspace, n_heads, seq_len, &q16, &k16, &v16);
   hipLaunchKernelGGL(fwd_d64_kernel, grid, dim3(kThreads), 0, stream, q, k, v, o, lse, n_heads,
-                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles, q16, k16, v16);
+                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles, q16, k16, v16,
+                     ldi > 0 ? ldi : n_heads * kD);
   return hipGetLastError();
 }
 

@@ -330,13 +330,29 @@ size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len, uint32_t d
 }
 
 namespace {
-int check_workspace(const char *fn, const void *workspace, size_t workspace_bytes,
-                    uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
+static int check_workspace(const char *fn, const void *workspace, size_t workspace_bytes,
+                           uint32_t n_heads, uint32_t seq_len, uint32_t d_head) {
   const size_t need = dfattn_bwd_workspace_bytes(n_heads, seq_len, d_head);
   if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, alignof(float)))
     return record_error(DFATTN_ERR_WORKSPACE,
                         std::string(fn) + ": workspace must be non-null, 4-byte aligned and hold " +
                             std::to_string(need) + " bytes");
+  return DFATTN_OK;
+}
+
+// The strided entry points run the d_head = 64 kernels only: 16-byte aligned
+// tensors and a row stride that is at least the row's own n_heads * 64
+// values, a multiple of 4 floats (16-byte rows) and at most 2^21 (the
+// kernels' 32-bit tile offsets).
+static int check_strided(const char *fn, uint32_t d_head, uint32_t n_heads, uint32_t stride,
+                         std::initializer_list<const void *> ptrs) {
+  if (d_head != 64)
+    return record_error(DFATTN_ERR_HEAD_DIM, std::string(fn) + ": the strided entry points need d_head 64");
+  if (stride < n_heads * d_head || stride % 4 != 0 || stride > (1u << 21))
+    return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": row stride must be >= n_heads*d_head, a multiple "
+                                                            "of 4 and at most 2^21");
+  if (!fast_path(d_head, ptrs))
+    return record_error(DFATTN_ERR_MISALIGNED, std::string(fn) + ": tensors must be 16-byte aligned");
   return DFATTN_OK;
 }
 }  // namespace
@@ -417,6 +433,54 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v, const float 
     err = dfattn::launch_bwd_generic(q, k, v, d_o, d_q, d_k, d_v, (int)n_heads, (int)seq_len,
                                      (int)d_head, scale, causal != 0, s);
   return record_hip(err, "attention backward launch");
+}
+
+int dfattn_fwd_train_strided(const float *q, const float *k, const float *v, float *o, float *lse,
+                             void *workspace, size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len,
+                             uint32_t d_head, float scale, uint32_t causal, uint32_t qkv_row_stride,
+                             void *stream) {
+  const char *fn = "dfattn_fwd_train_strided";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, lse});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_strided(fn, d_head, n_heads, qkv_row_stride, {q, k, v, o, lse});
+  if (st != DFATTN_OK) return st;
+  return record_hip(dfattn::launch_fwd_d64(q, k, v, o, lse, (int)n_heads, (int)seq_len, scale, causal != 0,
+                                           static_cast<hipStream_t>(stream), workspace, (int)qkv_row_stride),
+                    "attention forward launch");
+}
+
+int dfattn_bwd_preprocess_strided(const float *q, const float *k, const float *v, const float *o,
+                                  const float *d_o, const float *lse, void *workspace, size_t workspace_bytes,
+                                  uint32_t n_heads, uint32_t seq_len, uint32_t d_head, float scale, uint32_t flags,
+                                  uint32_t qkv_row_stride, void *stream) {
+  const char *fn = "dfattn_bwd_preprocess_strided";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {q, k, v, o, d_o, lse});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_strided(fn, d_head, n_heads, qkv_row_stride, {q, k, v, o, d_o, lse});
+  if (st != DFATTN_OK) return st;
+  if ((flags & ~(uint32_t)DFATTN_BWD_QKV_SAVED) != 0)
+    return record_error(DFATTN_ERR_FLAGS, std::string(fn) + ": unknown flag bits");
+  return record_hip(dfattn::launch_bwd_pre_d64(q, k, v, o, d_o, lse, workspace, (int)n_heads, (int)seq_len,
+                                               scale, static_cast<hipStream_t>(stream),
+                                               (flags & DFATTN_BWD_QKV_SAVED) != 0, (int)qkv_row_stride),
+                    "attention backward preprocess launch");
+}
+
+int dfattn_bwd_main_strided(const float *lse, float *d_q, float *d_k, float *d_v, void *workspace,
+                            size_t workspace_bytes, uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                            float scale, uint32_t causal, uint32_t grad_row_stride, void *stream) {
+  const char *fn = "dfattn_bwd_main_strided";
+  int st = check_shape(fn, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_ptrs(fn, {lse, d_q, d_k, d_v});
+  if (st == DFATTN_OK) st = check_workspace(fn, workspace, workspace_bytes, n_heads, seq_len, d_head);
+  if (st == DFATTN_OK) st = check_strided(fn, d_head, n_heads, grad_row_stride, {lse, d_q, d_k, d_v});
+  if (st != DFATTN_OK) return st;
+  return record_hip(dfattn::launch_bwd_main_d64(lse, d_q, d_k, d_v, workspace, (int)n_heads, (int)seq_len, scale,
+                                                causal != 0, static_cast<hipStream_t>(stream),
+                                                (int)grad_row_stride),
+                    "attention backward launch");
 }
 
 }  // extern "C"

@@ -257,10 +257,11 @@ __device__ __forceinline__ half8_t acc_to_slots(const f32x16 &blk, int half_sel)
 // Forward, D = 64, MFMA. q/k/v/o 16-byte aligned. lse may be null. With a
 // backward workspace (bwd_workspace_bytes_d64 bytes), the forward also
 // writes the backward's fp16 copies of c2*Q, K and V into it (see
-// launch_bwd_pre_d64's qkv_saved).
+// launch_bwd_pre_d64's qkv_saved). ldi: the row stride of q, k and v in
+// floats (0: n_heads * 64, contiguous); o is always contiguous.
 hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float *o,
                           float *lse, int n_heads, int seq_len, float scale, bool causal,
-                          hipStream_t stream, void *bwd_workspace = nullptr);
+                          hipStream_t stream, void *bwd_workspace = nullptr, int ldi = 0);
 
 // Backward, D = 64, MFMA. Needs bwd_workspace_bytes_d64() of workspace.
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len);
@@ -276,11 +277,14 @@ hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const 
 // qkv_saved: the workspace already holds the copies of c2*Q, K and V that a
 // launch_fwd_d64 with this workspace wrote for the same q, k, v and scale;
 // only dO is converted.
+// ldi: the row stride of q, k and v (read only without qkv_saved); ldg: the
+// row stride of d_q, d_k and d_v (0: n_heads * 64, contiguous).
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
                               const float *d_o, const float *lse, void *workspace, int n_heads, int seq_len,
-                              float scale, hipStream_t stream, bool qkv_saved = false);
+                              float scale, hipStream_t stream, bool qkv_saved = false, int ldi = 0);
 hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
-                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream);
+                               int n_heads, int seq_len, float scale, bool causal, hipStream_t stream,
+                               int ldg = 0);
 
 // Generic fp32 kernels for any d_head in 1..=128 and any 4-byte alignment.
 // The backward recomputes everything it needs per row and uses no workspace.

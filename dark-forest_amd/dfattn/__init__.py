@@ -52,6 +52,10 @@ SYMBOLS = {
     "dfattn_fwd_train": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_preprocess": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
     "dfattn_bwd_main": (ctypes.c_int, [_P] * 10 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _P]),
+    "dfattn_fwd_train_strided": (ctypes.c_int, [_P] * 6 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _U32, _P]),
+    "dfattn_bwd_preprocess_strided": (ctypes.c_int, [_P] * 7 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _U32,
+                                                                 _P]),
+    "dfattn_bwd_main_strided": (ctypes.c_int, [_P] * 5 + [ctypes.c_size_t, _U32, _U32, _U32, _F, _U32, _U32, _P]),
     "dfattn_bwd_noalloc": (ctypes.c_int, [_P] * 9 + [_U32, _U32, _U32, _F, _U32, _P]),
     "launch_fused_mha_decode_kv": (None, [_P] * 4 + [_U32, _U32, _U32, _F]),
     "launch_fused_mha_decode_kv_splitk": (None, [_P] * 7 + [_U32, _U32, _U32, _F, _U32]),
@@ -77,6 +81,10 @@ SYMBOLS = {
     "dfattn_context_forward_device_into": (ctypes.c_int, [_P] * 4 + [_F, _U32, _P, ctypes.c_size_t, _P]),
     "dfattn_context_backward_device_into": (ctypes.c_int,
                                             [_P] * 5 + [_F, _U32, _P, _P, _P, ctypes.c_size_t, _P]),
+    "dfattn_context_forward_device_into_strided": (ctypes.c_int,
+                                                   [_P] * 4 + [_F, _U32, _P, ctypes.c_size_t, _U32, _P]),
+    "dfattn_context_backward_device_into_strided": (ctypes.c_int, [_P] * 5 + [_F, _U32, _P, _P, _P, ctypes.c_size_t,
+                                                                              _U32, _U32, _P]),
     "dfattn_context_forward": (ctypes.c_int, [_P] * 4 + [ctypes.c_size_t, _F, _U32, _P]),
     "dfattn_context_backward": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _F, _U32, _P, _P, _P]),
     "dfattn_fused_attention_forward": (ctypes.c_int, [_P] * 3 + [ctypes.c_size_t, _U32, _U32, _F, _U32, _P]),
@@ -156,6 +164,36 @@ def _dev_ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _row_stride(t):
+    """Row stride in floats of a 2-D float32 tensor whose rows are contiguous, such as a column
+    block of a wider tensor; None when the tensor is contiguous. Raises for any other layout."""
+    torch = _torch()
+    if t.dtype != torch.float32:
+        raise ValueError("dfattn tensors must be float32")
+    if t.is_contiguous():
+        return None
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        raise ValueError("dfattn tensors must be contiguous or 2-D with contiguous rows")
+    return t.stride(0)
+
+
+def _rows_ptr(t):
+    """(device pointer, row stride or None) of a tensor _row_stride accepts."""
+    stride = _row_stride(t)
+    if not t.is_cuda:
+        raise ValueError("dfattn works on device tensors; got a CPU tensor")
+    return ctypes.c_void_p(t.data_ptr()), stride
+
+
+def _same_stride(name, *tensors):
+    """The device pointers and the one row stride of `tensors` (None: all contiguous); raises when
+    they differ."""
+    ptrs, strides = zip(*(_rows_ptr(t) for t in tensors))
+    if len(set(strides)) != 1:
+        raise ValueError(f"{name} must share one row stride")
+    return ptrs, strides[0]
+
+
 def _dims(q, n_heads):
     seq_len, dm = q.shape
     if dm % n_heads:
@@ -185,13 +223,18 @@ def forward_train(q, k, v, n_heads, workspace, scale=None, causal=True, out=None
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5
-    if out is None:
-        out = torch.empty_like(q)
+    if out is None:  # contiguous even when q is a column block of a wider tensor
+        out = torch.empty((seq_len, n_heads * d_head), dtype=torch.float32, device=q.device)
     if lse is None:
         lse = torch.empty((n_heads, seq_len), dtype=torch.float32, device=q.device)
-    _check(lib().dfattn_fwd_train(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(out), _dev_ptr(lse),
-                                  _dev_ptr(workspace), workspace.numel() * workspace.element_size(), n_heads,
-                                  seq_len, d_head, scale, int(bool(causal)), _stream_ptr(stream)))
+    (pq, pk, pv), stride = _same_stride("q, k and v", q, k, v)
+    ws = (_dev_ptr(workspace), workspace.numel() * workspace.element_size())
+    if stride is None:
+        _check(lib().dfattn_fwd_train(pq, pk, pv, _dev_ptr(out), _dev_ptr(lse), *ws, n_heads, seq_len, d_head,
+                                      scale, int(bool(causal)), _stream_ptr(stream)))
+    else:  # q, k, v are column blocks of a wider tensor (dfattn_fwd_train_strided)
+        _check(lib().dfattn_fwd_train_strided(pq, pk, pv, _dev_ptr(out), _dev_ptr(lse), *ws, n_heads, seq_len, d_head,
+                                              scale, int(bool(causal)), stride, _stream_ptr(stream)))
     return out, lse
 
 
@@ -249,21 +292,33 @@ def backward_preprocess(q, k, v, o, d_o, lse, workspace, n_heads, scale=None, fl
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5
-    _check(lib().dfattn_bwd_preprocess(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o),
-                                       _dev_ptr(lse), _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
-                                       n_heads, seq_len, d_head, scale, int(flags), _stream_ptr(stream)))
+    (pq, pk, pv), stride = _same_stride("q, k and v", q, k, v)
+    rest = (_dev_ptr(o), _dev_ptr(d_o), _dev_ptr(lse), _dev_ptr(workspace), workspace.numel() * workspace.element_size(),
+            n_heads, seq_len, d_head, scale, int(flags))
+    if stride is None:
+        _check(lib().dfattn_bwd_preprocess(pq, pk, pv, *rest, _stream_ptr(stream)))
+    else:
+        _check(lib().dfattn_bwd_preprocess_strided(pq, pk, pv, *rest, stride, _stream_ptr(stream)))
 
 
 def backward_main(q, k, v, o, d_o, lse, d_q, d_k, d_v, workspace, n_heads, scale=None, causal=True, stream=None):
     """Second phase of attention_backward (the fused dQ/dK/dV kernel); same q, k, v, o, d_o,
-    lse, workspace and scale as backward_preprocess."""
+    lse, workspace and scale as backward_preprocess. q, k, v, and d_q, d_k, d_v, may each be
+    column blocks of one wider tensor; the strided kernel then reads only the workspace."""
     seq_len, d_head = _dims(q, n_heads)
     if scale is None:
         scale = d_head ** -0.5
-    _check(lib().dfattn_bwd_main(_dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(o), _dev_ptr(d_o), _dev_ptr(lse),
-                                 _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), _dev_ptr(workspace),
-                                 workspace.numel() * workspace.element_size(), n_heads, seq_len, d_head, scale,
-                                 int(bool(causal)), _stream_ptr(stream)))
+    (pdq, pdk, pdv), stride = _same_stride("d_q, d_k and d_v", d_q, d_k, d_v)
+    (pq, pk, pv), qkv_stride = _same_stride("q, k and v", q, k, v)
+    ws = (_dev_ptr(workspace), workspace.numel() * workspace.element_size())
+    if stride is None and qkv_stride is not None:
+        stride = n_heads * d_head  # contiguous gradients, but the unstrided call would take q, k, v as packed
+    if stride is None:
+        _check(lib().dfattn_bwd_main(pq, pk, pv, _dev_ptr(o), _dev_ptr(d_o), _dev_ptr(lse), pdq, pdk, pdv, *ws,
+                                     n_heads, seq_len, d_head, scale, int(bool(causal)), _stream_ptr(stream)))
+    else:  # gradients into column blocks of a wider tensor (dfattn_bwd_main_strided)
+        _check(lib().dfattn_bwd_main_strided(_dev_ptr(lse), pdq, pdk, pdv, *ws, n_heads, seq_len, d_head, scale,
+                                             int(bool(causal)), stride, _stream_ptr(stream)))
 
 
 def launch_fused_mha_forward(q, k, v, out, n_heads, seq_len, d_head, scale, causal):
@@ -459,10 +514,16 @@ class AttentionContext:
         return t.numel()
 
     def forward_device_into(self, q, k, v, scale, causal, out, stream=None):
-        """lib.rs:2042: O into `out`; also the context's logsumexp."""
-        _check(lib().dfattn_context_forward_device_into(
-            self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), scale, int(bool(causal)), _dev_ptr(out),
-            self._elems(out) & ((1 << 64) - 1), _stream_ptr(stream)))
+        """lib.rs:2042: O into `out`; also the context's logsumexp. q, k, v may be column blocks of
+        one wider tensor (rows contiguous, one row stride: the strided context call)."""
+        (pq, pk, pv), stride = _same_stride("q, k and v", q, k, v)
+        n = self._elems(out) & ((1 << 64) - 1)
+        if stride is None:
+            _check(lib().dfattn_context_forward_device_into(self._h, pq, pk, pv, scale, int(bool(causal)),
+                                                            _dev_ptr(out), n, _stream_ptr(stream)))
+        else:
+            _check(lib().dfattn_context_forward_device_into_strided(self._h, pq, pk, pv, scale, int(bool(causal)),
+                                                                    _dev_ptr(out), n, stride, _stream_ptr(stream)))
         if self.reuse_forward:
             self._last = (q, k, v, out)
 
@@ -473,11 +534,19 @@ class AttentionContext:
         return out
 
     def backward_device_into(self, q, k, v, d_out, scale, causal, d_q, d_k, d_v, stream=None):
-        """lib.rs:2240: dQ, dK, dV into the given tensors."""
-        n = min(self._elems(d_q), self._elems(d_k), self._elems(d_v))
-        _check(lib().dfattn_context_backward_device_into(
-            self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), _dev_ptr(d_out), scale, int(bool(causal)),
-            _dev_ptr(d_q), _dev_ptr(d_k), _dev_ptr(d_v), n & ((1 << 64) - 1), _stream_ptr(stream)))
+        """lib.rs:2240: dQ, dK, dV into the given tensors. q, k, v, and d_q, d_k, d_v, may each be
+        column blocks of one wider tensor (the strided context call)."""
+        n = min(self._elems(d_q), self._elems(d_k), self._elems(d_v)) & ((1 << 64) - 1)
+        (pq, pk, pv), qs = _same_stride("q, k and v", q, k, v)
+        (pdq, pdk, pdv), gs = _same_stride("d_q, d_k and d_v", d_q, d_k, d_v)
+        if qs is None and gs is None:
+            _check(lib().dfattn_context_backward_device_into(self._h, pq, pk, pv, _dev_ptr(d_out), scale,
+                                                             int(bool(causal)), pdq, pdk, pdv, n, _stream_ptr(stream)))
+        else:
+            dm = self.d_model
+            _check(lib().dfattn_context_backward_device_into_strided(
+                self._h, pq, pk, pv, _dev_ptr(d_out), scale, int(bool(causal)), pdq, pdk, pdv, n,
+                qs or dm, gs or dm, _stream_ptr(stream)))
 
     def backward_device(self, q, k, v, d_out, scale, causal, stream=None):
         """lib.rs:2226: allocate dQ, dK, dV and run backward_device_into."""

@@ -255,6 +255,36 @@ int dfattn_bwd_main(const float *q, const float *k, const float *v,
                     uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
                     float scale, uint32_t causal, void *stream);
 
+/* The training pair with row strides. No counterpart in the reference (its
+ * engine keeps Q, K, V and their gradients in separate [S, H*D] tensors):
+ * for callers whose Q, K, V are the three column blocks of one fused
+ * projection [S, 3*H*D] and whose gradients go back into one such tensor,
+ * which saves splitting and re-interleaving them. Same semantics and
+ * results, bit for bit, as dfattn_fwd_train, dfattn_bwd_preprocess and
+ * dfattn_bwd_main with contiguous tensors, except that row i of q, k and v
+ * starts qkv_row_stride floats after row i-1 (each buffer must hold
+ * (seq_len-1)*stride + n_heads*d_head floats), and likewise d_q, d_k, d_v
+ * with grad_row_stride; o, d_o and lse stay contiguous. d_head must be 64,
+ * every tensor 16-byte aligned, and a stride at least n_heads*d_head, a
+ * multiple of 4 and at most 2^21 (else DFATTN_ERR_HEAD_DIM,
+ * DFATTN_ERR_MISALIGNED or DFATTN_ERR_SHAPE). The main phase reads only the
+ * workspace, lse and its outputs, so it takes no q, k, v.                  */
+int dfattn_fwd_train_strided(const float *q, const float *k, const float *v, float *o,
+                             float *lse, void *workspace, size_t workspace_bytes,
+                             uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                             float scale, uint32_t causal, uint32_t qkv_row_stride,
+                             void *stream);
+int dfattn_bwd_preprocess_strided(const float *q, const float *k, const float *v,
+                                  const float *o, const float *d_o, const float *lse,
+                                  void *workspace, size_t workspace_bytes,
+                                  uint32_t n_heads, uint32_t seq_len, uint32_t d_head,
+                                  float scale, uint32_t flags, uint32_t qkv_row_stride,
+                                  void *stream);
+int dfattn_bwd_main_strided(const float *lse, float *d_q, float *d_k, float *d_v,
+                            void *workspace, size_t workspace_bytes, uint32_t n_heads,
+                            uint32_t seq_len, uint32_t d_head, float scale, uint32_t causal,
+                            uint32_t grad_row_stride, void *stream);
+
 /* Backward that allocates nothing. No counterpart in the reference: it is
  * for callers that cannot call hipMalloc or take a workspace (code under
  * HIP graph capture, tight serving loops, harnesses that forbid
@@ -339,6 +369,26 @@ int dfattn_context_backward_device_into(dfattn_context *ctx, const float *q, con
                                         const float *v, const float *d_out, float scale,
                                         uint32_t causal, float *d_q, float *d_k, float *d_v,
                                         size_t grad_elems, void *stream);
+
+/* The two calls above with row strides: q, k, v read at qkv_row_stride
+ * floats per row, d_q, d_k, d_v written at grad_row_stride (out and d_out
+ * contiguous), through the strided training pair above. No counterpart in
+ * the reference: for an engine whose Q/K/V projection is one fused GEMM
+ * with an [S, 3*H*D] output and whose Q/K/V gradients feed one such GEMM.
+ * A stride of exactly n_heads*d_head is the contiguous layout and takes
+ * the unstrided call (any d_head). A reused forward
+ * (dfattn_context_set_reuse_forward) must have had the same q, k, v
+ * pointers and row stride.                                               */
+int dfattn_context_forward_device_into_strided(dfattn_context *ctx, const float *q,
+                                               const float *k, const float *v, float scale,
+                                               uint32_t causal, float *out, size_t out_elems,
+                                               uint32_t qkv_row_stride, void *stream);
+int dfattn_context_backward_device_into_strided(dfattn_context *ctx, const float *q,
+                                                const float *k, const float *v,
+                                                const float *d_out, float scale, uint32_t causal,
+                                                float *d_q, float *d_k, float *d_v,
+                                                size_t grad_elems, uint32_t qkv_row_stride,
+                                                uint32_t grad_row_stride, void *stream);
 
 /* lib.rs:2295 forward / :2328 backward: host slices of seq_len * d_head
  * floats uploaded into context buffers and run on the single-head path, as

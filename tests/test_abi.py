@@ -147,6 +147,59 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         dfattn.lib()
 
 
+ODD4 = ctypes.c_void_p(0x10004)  # 4-byte but not 16-byte aligned
+
+
+def strided(fn, stride=3 * 768, h=12, s=1024, d=64, ptr=FAKE, ws=FAKE, ws_bytes=None, flags=1):
+    """One of the three row-strided training calls on fake pointers (validation fails first)."""
+    lib = dfattn.lib()
+    if ws_bytes is None:
+        ws_bytes = lib.dfattn_bwd_workspace_bytes(h, s, 64)
+    if fn == "fwd":
+        return lib.dfattn_fwd_train_strided(ptr, FAKE, FAKE, FAKE, FAKE, ws, ws_bytes, h, s, d, 0.125, 1, stride, None)
+    if fn == "pre":
+        return lib.dfattn_bwd_preprocess_strided(ptr, FAKE, FAKE, FAKE, FAKE, FAKE, ws, ws_bytes, h, s, d, 0.125,
+                                                 flags, stride, None)
+    return lib.dfattn_bwd_main_strided(FAKE, ptr, FAKE, FAKE, ws, ws_bytes, h, s, d, 0.125, 1, stride, None)
+
+
+@pytest.mark.parametrize("fn", ["fwd", "pre", "main"])
+@pytest.mark.parametrize("kwargs,status", [
+    (dict(d=32), -4), (dict(d=128), -4), (dict(stride=767), -3), (dict(stride=770), -3),
+    (dict(stride=(1 << 21) + 4), -3), (dict(stride=0), -3), (dict(ptr=ODD4), -2), (dict(ptr=None), -1),
+    (dict(ws=None), -6), (dict(h=0), -3),
+])
+def test_strided_training_pair_validation(fn, kwargs, status):
+    """Row strides below the row's n_heads*64 floats, not a multiple of 4 or above 2^21, a head size
+    other than 64 and tensors that are not 16-byte aligned are refused before any HIP call."""
+    lib = dfattn.lib()
+    lib.dfattn_clear_error()
+    assert strided(fn, **kwargs) == status
+    assert lib.dfattn_last_error() == status
+    assert b"strided" in lib.dfattn_last_error_message() or status in (-1, -3, -6)
+    lib.dfattn_clear_error()
+
+
+def test_strided_preprocess_rejects_unknown_flags():
+    assert strided("pre", flags=2) == -8
+    dfattn.lib().dfattn_clear_error()
+
+
+def test_strided_python_helpers_validate_layouts():
+    """Column blocks of one [S, 3*H*D] tensor have one row stride; other layouts are refused."""
+    import torch
+
+    wide = torch.zeros(8, 3 * 128)
+    assert [dfattn._row_stride(wide[:, i * 128:(i + 1) * 128]) for i in range(3)] == [384] * 3
+    assert dfattn._row_stride(torch.zeros(8, 128)) is None
+    assert dfattn._row_stride(wide[:1, :128]) is None  # one row is contiguous
+    for bad in (wide[:, :128].t(), wide[:, ::2], torch.zeros(8, 128, dtype=torch.float64)):
+        with pytest.raises(ValueError):
+            dfattn._row_stride(bad)
+    with pytest.raises(ValueError):
+        dfattn._same_stride("q", wide[:, :128])  # a CPU tensor
+
+
 # ---------------------------------------------------------------- the context mirror (lib.rs:1949-2368)
 @pytest.mark.parametrize("dims,status", [
     ((12, 128, 0), -4), ((12, 128, 129), -4), ((0, 128, 64), -3), ((12, 0, 64), -3),
@@ -170,6 +223,10 @@ def test_null_context_calls_fail_cleanly():
     assert lib.dfattn_context_forward_device_into(None, FAKE, FAKE, FAKE, 0.125, 1, FAKE, 10, None) == -1
     assert lib.dfattn_context_backward_device_into(None, FAKE, FAKE, FAKE, FAKE, 0.125, 1, FAKE, FAKE, FAKE, 10,
                                                    None) == -1
+    assert lib.dfattn_context_forward_device_into_strided(None, FAKE, FAKE, FAKE, 0.125, 1, FAKE, 10, 2304,
+                                                          None) == -1
+    assert lib.dfattn_context_backward_device_into_strided(None, FAKE, FAKE, FAKE, FAKE, 0.125, 1, FAKE, FAKE,
+                                                           FAKE, 10, 2304, 2304, None) == -1
     assert lib.dfattn_context_lse(None) is None
     lib.dfattn_context_destroy(None)  # no-op
 
