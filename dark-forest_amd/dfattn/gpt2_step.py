@@ -294,12 +294,17 @@ class _NativeEngine:
         def buf(name, *shape):
             plan.append((name, shape))
 
+        # The strided attention calls (Q, K, V read from the fused projection's output in place)
+        # take d_head 64; other head sizes get contiguous copies.
+        self.packed = d // H != 64
         for l in range(L + 1):
             buf(f"x{l}", S, d)
         for l in range(L):
             for n in ("ln1", "att", "xmid", "ln2"):
                 buf(f"{n}{l}", S, d)
-            buf(f"qkv{l}", 3, S, d)  # q, k, v of the layer, each contiguous [S, d]
+            buf(f"qkv{l}", S, 3 * d)  # the fused projection's output: q | k | v by row
+            if self.packed:
+                buf(f"qkvc{l}", 3, S, d)
             buf(f"st1{l}", 2, S)
             buf(f"st2{l}", 2, S)
             buf(f"h{l}", S, F)
@@ -316,8 +321,9 @@ class _NativeEngine:
         buf("loss", 1)
         for n in ("g0", "g1", "dlnf", "dln", "datt"):
             buf(n, S, d)
-        buf("dqkv", 3, S, d)  # the attention backward's dq, dk, dv
-        buf("wide", S, 3 * d)  # [S, 3 d_model]: the fused projection's output, or dq|dk|dv by row
+        buf("wide", S, 3 * d)  # [S, 3 d_model]: dq | dk | dv by row, the fused projection's gradient
+        if self.packed:
+            buf("dqkv", 3, S, d)
         buf("dh", S, F)
         buf("da", S, F)
         offsets, n = {}, 0
@@ -342,6 +348,12 @@ class _NativeEngine:
         for lw in m.layers:
             self.wqkv.append(self._adjacent([lw["wq"], lw["wk"], lw["wv"]]))
             self.bqkv.append(self._adjacent([lw["bq"], lw["bk"], lw["bv"]]))
+
+    def _qkv(self, l):
+        """Layer l's q, k, v: the column blocks of its projection output, or their copies."""
+        if self.packed:
+            return self.b[f"qkvc{l}"].unbind(0)
+        return self.b[f"qkv{l}"].split(self.m.d_model, dim=1)
 
     @staticmethod
     def _adjacent(ts):
@@ -437,13 +449,12 @@ class _NativeEngine:
         for l, lw in enumerate(m.layers):
             x, ln1, ln2 = b[f"x{l}"], b[f"ln1{l}"], b[f"ln2{l}"]
             qkv, att, xmid = b[f"qkv{l}"], b[f"att{l}"], b[f"xmid{l}"]
-            # Q, K, V in one GEMM ([S, 3d]); the bias is added as the result is split into three
-            # contiguous [S, d] tensors.
-            self._exact(ex["qkv_fwd"])
-            torch.mm(ln1, self.wqkv[l].t(), out=b["wide"])
-            torch.add(b["wide"].view(S, 3, -1).transpose(0, 1), self.bqkv[l].view(3, 1, -1), out=qkv)
-            q, k, v = qkv[0], qkv[1], qkv[2]
-            self.ctx[l].forward_device_into(q, k, v, self.scale, True, att)
+            # Q, K, V in one GEMM ([S, 3d]); attention reads its three column blocks in place
+            # (the strided context call).
+            self._linear(ln1, self.wqkv[l], self.bqkv[l], qkv, ex["qkv_fwd"])
+            if self.packed:
+                b[f"qkvc{l}"].copy_(qkv.view(S, 3, -1).transpose(0, 1))
+            self.ctx[l].forward_device_into(*self._qkv(l), self.scale, True, att)
             self._linear(att, lw["wo"], lw["bo"], b["tmp"], ex["o_fwd"])
             _ops.add_layer_norm_forward_into(x, b["tmp"], lw["ln2_g"], lw["ln2_b"], xmid, ln2, b[f"st2{l}"])
             # h = ln2 W1^T; the bias goes into h as GELU reads it
@@ -498,9 +509,8 @@ class _NativeEngine:
 
     # ---------------------------------------------------------------- backward (static_gpt2.rs:1424-1575)
     def _backward(self):
-        torch = _torch()
         m, b, ex = self.m, self.b, self.exact_sites
-        L, S = m.n_layers, m.seq_len
+        L = m.n_layers
         g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
         self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g)
         for l in reversed(range(L)):
@@ -519,12 +529,12 @@ class _NativeEngine:
             # attention: output projection, the fused attention backward, the Q/K/V projections
             self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], ex["wo_dx"], ex["wo_dw"])
             self._bias_grad(g, lw["bo"])
-            qkv, dqkv = b[f"qkv{l}"], b["dqkv"]
-            self.ctx[l].backward_device_into(qkv[0], qkv[1], qkv[2], b["datt"], self.scale, True,
-                                             dqkv[0], dqkv[1], dqkv[2])
             # dq | dk | dv side by side ([S, 3d]) for the fused projection's backward
             wide = b["wide"]
-            wide.view(S, 3, -1).copy_(dqkv.transpose(0, 1))
+            grads = b["dqkv"].unbind(0) if self.packed else wide.split(m.d_model, dim=1)
+            self.ctx[l].backward_device_into(*self._qkv(l), b["datt"], self.scale, True, *grads)
+            if self.packed:
+                wide.view(m.seq_len, 3, -1).copy_(b["dqkv"].transpose(0, 1))
             self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], ex["qkv_dx"], ex["qkv_dw"])
             self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
