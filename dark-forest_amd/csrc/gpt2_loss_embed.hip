@@ -8,9 +8,11 @@
 // (embedding gradients).
 //
 //  * Cross-entropy: one workgroup per row of logits. The row (50257 values
-//    for GPT-2) is read once for an online max and sum of exponentials per
-//    thread, the per-thread pairs are merged in a fixed order, and a second
-//    read writes the gradient (softmax - one_hot) / total_rows. The
+//    for GPT-2) is read once into registers (98 values per thread), its max
+//    and sum of exponentials are merged in a fixed order, and the gradient
+//    (softmax - one_hot) / total_rows is written from the registers (rows
+//    too long for that: an online max and sum per thread, then a second
+//    read for the gradient). The
 //    stream entry point writes each row's loss to its own slot (summed in a
 //    fixed order afterwards), so a step's loss is reproducible bit for bit;
 //    the reference's launcher adds the rows' losses with float atomics, and
@@ -109,6 +111,102 @@ __global__ __launch_bounds__(kCeThreads) void ce_row_kernel(float *logits, const
     else
       atomicAdd(loss, l);
   }
+}
+
+// The same contract with the row held in registers, K values per thread
+// (cols <= K * kCeThreads): one read of the row, its maximum, then the sum of
+// exponentials about it (both merged in a fixed order: lanes by butterfly,
+// then the waves in order), with the exponentials kept in registers for the
+// gradient's write. One read and one write of the row instead of two reads
+// and a write.
+template <bool WRITE_PROBS, bool ROW_LOSS, int K>
+__global__ __launch_bounds__(kCeThreads) void ce_row_reg_kernel(float *logits, const uint32_t *__restrict__ targets,
+                                                                float *grad, float *__restrict__ row_loss,
+                                                                float *__restrict__ loss, int cols, float inv_total) {
+  __shared__ float red[kCeThreads / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float *x = logits + (size_t)row * cols;
+  float *gx = grad + (size_t)row * cols;
+  const uint32_t target = targets[row];
+  // The target's logit, read before any thread overwrites the row.
+  const float xt = (tid == 0 && target < (uint32_t)cols) ? x[target] : -INFINITY;
+  // Buffer accesses bounded by the row (the lane's byte offset in the vector
+  // offset, which the hardware checks: loads past the row read 0, stores
+  // there are dropped), so the row needs no 64-bit address per value.
+  const auto rx = buffer_rsrc(x, (unsigned)cols * 4u);
+  const auto rg = buffer_rsrc(gx, (unsigned)cols * 4u);
+  float v[K];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (tid + k * kCeThreads) * 4, 0, 0));
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (tid + k * kCeThreads >= cols) v[k] = -INFINITY;
+    mx = fmaxf(mx, v[k]);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kCeThreads / 64; ++w) m = fmaxf(m, red[w]);
+  __syncthreads();  // red is reused for the sums
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    v[k] = exp2f((v[k] - m) * kLog2e);  // 0 past the row's end
+    s += v[k];
+  }
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  float tot = red[0];
+#pragma unroll
+  for (int w = 1; w < kCeThreads / 64; ++w) tot += red[w];
+  const float inv_sum = 1.f / tot;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = tid + k * kCeThreads;
+    const float p = v[k] * inv_sum;
+    if (WRITE_PROBS) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, p), rx, i * 4, 0, 0);
+    const float gv = (p - ((uint32_t)i == target ? 1.f : 0.f)) * inv_total;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, gv), rg, i * 4, 0, 0);
+  }
+  if (tid == 0) {
+    const float pt = exp2f((xt - m) * kLog2e) * inv_sum;
+    const float l = -logf(fmaxf(pt, 1e-12f)) * inv_total;  // softmax.cu:377 clamps at 1e-12
+    if (ROW_LOSS)
+      row_loss[row] = l;
+    else
+      atomicAdd(loss, l);
+  }
+}
+
+// One launch of the cross-entropy over `rows` rows: the register-resident
+// kernel when a row fits (cols <= 100 * kCeThreads, GPT-2's 50257 among
+// them), else the two-read one.
+template <bool WRITE_PROBS, bool ROW_LOSS>
+void launch_ce(float *logits, const uint32_t *targets, float *grad, float *row_loss, float *loss, uint32_t rows,
+               uint32_t cols, float inv_total, hipStream_t stream) {
+  const dim3 grid(rows), block(kCeThreads);
+  const int c = (int)cols;
+  if (cols <= 1u * kCeThreads)
+    hipLaunchKernelGGL((ce_row_reg_kernel<WRITE_PROBS, ROW_LOSS, 1>), grid, block, 0, stream, logits, targets, grad,
+                       row_loss, loss, c, inv_total);
+  else if (cols <= 8u * kCeThreads)
+    hipLaunchKernelGGL((ce_row_reg_kernel<WRITE_PROBS, ROW_LOSS, 8>), grid, block, 0, stream, logits, targets, grad,
+                       row_loss, loss, c, inv_total);
+  else if (cols <= 32u * kCeThreads)
+    hipLaunchKernelGGL((ce_row_reg_kernel<WRITE_PROBS, ROW_LOSS, 32>), grid, block, 0, stream, logits, targets, grad,
+                       row_loss, loss, c, inv_total);
+  else if (cols <= 100u * kCeThreads)
+    hipLaunchKernelGGL((ce_row_reg_kernel<WRITE_PROBS, ROW_LOSS, 100>), grid, block, 0, stream, logits, targets,
+                       grad, row_loss, loss, c, inv_total);
+  else
+    hipLaunchKernelGGL((ce_row_kernel<WRITE_PROBS, ROW_LOSS>), grid, block, 0, stream, logits, targets, grad, row_loss,
+                       loss, c, inv_total);
 }
 
 // Sum of n values in a fixed order (one workgroup): the step's loss from the
@@ -235,8 +333,8 @@ extern "C" int dfgpt2_logit_ce_chunk(float *logits, const uint32_t *targets, flo
   if (int st = need(fn, {logits, targets, grad_logits, row_loss}); st != DFATTN_OK) return st;
   if (int st = dims_ok(fn, chunk_rows, cols); st != DFATTN_OK) return st;
   if (total_rows == 0) return record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": total_rows must be >= 1");
-  hipLaunchKernelGGL((ce_row_kernel<false, true>), dim3(chunk_rows), dim3(kCeThreads), 0, stream, logits, targets,
-                     grad_logits, row_loss, nullptr, (int)cols, 1.f / (float)total_rows);
+  launch_ce<false, true>(logits, targets, grad_logits, row_loss, nullptr, chunk_rows, cols, 1.f / (float)total_rows,
+                         stream);
   return launched(fn);
 }
 
@@ -292,8 +390,8 @@ extern "C" void launch_fused_chunked_logit_ce(float *logits, const uint32_t *tar
     if (st == DFATTN_OK && total_rows == 0)
       st = record_error(DFATTN_ERR_SHAPE, std::string(fn) + ": total_rows must be >= 1");
     if (st == DFATTN_OK) {
-      hipLaunchKernelGGL((ce_row_kernel<true, false>), dim3(chunk_rows), dim3(kCeThreads), 0, nullptr, logits,
-                         targets, grad_logits, nullptr, loss, (int)cols, 1.f / (float)total_rows);
+      launch_ce<true, false>(logits, targets, grad_logits, nullptr, loss, chunk_rows, cols, 1.f / (float)total_rows,
+                             nullptr);
       st = launched(fn);
     }
   }

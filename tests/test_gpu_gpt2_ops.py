@@ -185,12 +185,14 @@ def test_reference_launchers_match_the_stream_entry_points(device):
 
 
 # ---------------------------------------------------------------- cross-entropy (softmax.cu:325-413)
-@pytest.mark.parametrize("rows,vocab", [(512, 50257), (7, 1000), (3, 1)])
+@pytest.mark.parametrize("rows,vocab", [(512, 50257), (7, 1000), (3, 1), (4, 512), (4, 513), (5, 4097),
+                                       (3, 51200), (2, 51201)])
 def test_chunked_cross_entropy_matches_torch(device, rows, vocab):
     """dfgpt2_logit_ce_chunk + dfgpt2_sum against torch's fp64 log-softmax: the gradient
     (softmax - one_hot) / total_rows per value and the mean loss, with the gradient written to its
     own buffer and in place; the reference launcher writes the softmax back and sums the loss with
-    atomics."""
+    atomics. The vocabularies cover each register-resident row size (up to 1, 8, 32 and 100 values
+    per thread, full and one past) and the two-read kernel for longer rows."""
     import torch
 
     say(f"cross-entropy rows={rows} vocab={vocab}")
