@@ -210,6 +210,112 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_generic_kernel(const float *__r
   }
 }
 
+// ------------------------------------ LayerNorm backward with its column sums
+// ln_bwd_dx_vec_kernel's grad_x (the same arithmetic, so the same values),
+// plus each workgroup's partial column sums of grad_out * x_hat and grad_out
+// (the parameter gradients' terms) and, when `planes` is 3, of grad_x itself
+// (the bias gradient of the linear layer whose output gradient grad_x is):
+// per lane over its row, then the four rows added in wave order through LDS,
+// into partial[blockIdx.x][plane][features]. colsum_partials_kernel adds the
+// workgroups' partials in order. The rows are read once for all of it.
+template <int V>
+__global__ __launch_bounds__(256) void ln_bwd_fused_kernel(const float *__restrict__ dout, const float *__restrict__ x,
+                                                           const float *__restrict__ gamma,
+                                                           const float *__restrict__ means,
+                                                           const float *__restrict__ rstds,
+                                                           const float *__restrict__ residual,
+                                                           float *__restrict__ grad_x, float *__restrict__ partial,
+                                                           int planes, int batch, int features) {
+  __shared__ __attribute__((aligned(16))) float part[4][3][V * 256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + wave;
+  const bool ok = row < batch;
+  const int nv = features >> 2;
+  const float mean = ok ? means[row] : 0.f, rstd = ok ? rstds[row] : 0.f;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * features);
+  const float4 *dr = reinterpret_cast<const float4 *>(dout + (size_t)row * features);
+  float4 xh[V], ds[V], dv[V];
+  float sds = 0.f, sdsx = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    xh[i] = ds[i] = dv[i] = splat4(0.f);
+    if (ok && c < nv) {
+      const float4 xv = xr[c];
+      dv[i] = dr[c];
+      const float4 g = gamma ? reinterpret_cast<const float4 *>(gamma)[c] : splat4(1.f);
+      xh[i] = make_float4((xv.x - mean) * rstd, (xv.y - mean) * rstd, (xv.z - mean) * rstd, (xv.w - mean) * rstd);
+      ds[i] = make_float4(dv[i].x * g.x, dv[i].y * g.y, dv[i].z * g.z, dv[i].w * g.w);
+      sds += hsum4(ds[i]);
+      sdsx += (ds[i].x * xh[i].x + ds[i].y * xh[i].y) + (ds[i].z * xh[i].z + ds[i].w * xh[i].w);
+    }
+  }
+  const float sum_ds = wave_sum(sds), sum_dsx = wave_sum(sdsx);
+  const float f = (float)features, k = rstd / f;
+  float4 *gr = reinterpret_cast<float4 *>(grad_x + (size_t)row * features);
+  const float4 *rr = reinterpret_cast<const float4 *>(residual + (size_t)row * features);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int c = lane + 64 * i;
+    float4 o = splat4(0.f);
+    if (ok && c < nv) {
+      o = make_float4(k * (f * ds[i].x - sum_ds - xh[i].x * sum_dsx), k * (f * ds[i].y - sum_ds - xh[i].y * sum_dsx),
+                      k * (f * ds[i].z - sum_ds - xh[i].z * sum_dsx), k * (f * ds[i].w - sum_ds - xh[i].w * sum_dsx));
+      if (residual != nullptr) {
+        const float4 r = rr[c];
+        o = make_float4(o.x + r.x, o.y + r.y, o.z + r.z, o.w + r.w);
+      }
+      gr[c] = o;
+    }
+    if (c < nv) {
+      *reinterpret_cast<float4 *>(&part[wave][0][4 * c]) =
+          make_float4(dv[i].x * xh[i].x, dv[i].y * xh[i].y, dv[i].z * xh[i].z, dv[i].w * xh[i].w);
+      *reinterpret_cast<float4 *>(&part[wave][1][4 * c]) = dv[i];
+      *reinterpret_cast<float4 *>(&part[wave][2][4 * c]) = o;
+    }
+  }
+  __syncthreads();
+  float *dst = partial + (size_t)blockIdx.x * planes * features;
+  for (int j = threadIdx.x; j < planes * features; j += 256) {
+    const int plane = j / features, c = j - plane * features;
+    dst[j] = ((part[0][plane][c] + part[1][plane][c]) + part[2][plane][c]) + part[3][plane][c];
+  }
+}
+
+// out_p[c] = sum over the n_parts workgroups' partial[w][p][c] (p < planes,
+// out_p NULL: not written): 16 slices of consecutive workgroups, each added
+// in order, then the slices in order; 16 columns of one plane per workgroup.
+__global__ __launch_bounds__(256) void colsum_partials_kernel(const float *__restrict__ partial, int n_parts,
+                                                              int planes, int features, float *__restrict__ out0,
+                                                              float *__restrict__ out1, float *__restrict__ out2) {
+  __shared__ float acc[16][17];
+  const int t = threadIdx.x, col16 = t & 15, slice = t >> 4;
+  const int j = blockIdx.x * 16 + col16;  // flattened plane * features + c
+  const int per = (n_parts + 15) / 16;
+  const int w0 = slice * per, w1 = min(n_parts, w0 + per);
+  const size_t stride = (size_t)planes * features;
+  // Up to 16 independent loads in flight per thread, then added in order.
+  float s = 0.f;
+  if (j < planes * features)
+    for (int wb = w0; wb < w1; wb += 16) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = wb + k < w1 ? partial[(size_t)(wb + k) * stride + j] : 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s += v[k];
+    }
+  acc[slice][col16] = s;
+  __syncthreads();
+  if (t < 16 && j < planes * features) {
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) tot += acc[q][t];
+    const int plane = j / features, c = j - plane * features;
+    float *o = plane == 0 ? out0 : (plane == 1 ? out1 : out2);
+    if (o != nullptr) o[c] = tot;
+  }
+}
+
 // ------------------------------------------------------------- column sums
 // Sums over the rows of a [rows, cols] row-major matrix g, kColStrip = 16
 // columns per workgroup of 1024 threads (48 workgroups at 768 columns): lane
@@ -629,6 +735,61 @@ extern "C" int dfgpt2_layernorm_backward_residual(const float *grad_out, const f
     return st;
   return ln_backward(fn, grad_out, x, gamma, means, rstds, residual, grad_x, grad_gamma, grad_beta, 0, batch, features,
                      stream);
+}
+
+extern "C" size_t dfgpt2_layernorm_backward_fused_workspace_bytes(uint32_t batch, uint32_t features) {
+  return (size_t)((batch + 3) / 4) * 3 * features * sizeof(float);
+}
+
+template <int V>
+void launch_ln_fused_v(const float *dout, const float *x, const float *gamma, const float *means, const float *rstds,
+                       const float *residual, float *grad_x, float *partial, int planes, int batch, int features,
+                       hipStream_t stream) {
+  hipLaunchKernelGGL(ln_bwd_fused_kernel<V>, dim3((batch + 3) / 4), dim3(256), 0, stream, dout, x, gamma, means,
+                     rstds, residual, grad_x, partial, planes, batch, features);
+}
+
+extern "C" int dfgpt2_layernorm_backward_fused(const float *grad_out, const float *x, const float *gamma,
+                                               const float *means, const float *rstds, const float *residual,
+                                               float *grad_x, float *grad_gamma, float *grad_beta, float *grad_bias,
+                                               void *workspace, size_t workspace_bytes, uint32_t batch,
+                                               uint32_t features, hipStream_t stream) {
+  const char *fn = "dfgpt2_layernorm_backward_fused";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {grad_out, x, means, rstds, grad_x}, {gamma, residual, grad_gamma, grad_beta, grad_bias});
+      st != DFATTN_OK)
+    return st;
+  const int b = (int)batch, f = (int)features;
+  const bool sums = grad_gamma != nullptr || grad_beta != nullptr || grad_bias != nullptr;
+  if (!sums || !ln_vec(features, {grad_out, x, gamma, residual, grad_x})) {
+    // Any width and alignment: the separate launches, the same results contract.
+    ln_backward_dx(grad_out, x, gamma, means, rstds, residual, grad_x, b, f, stream);
+    if (int st = launched(fn); st != DFATTN_OK || !sums) return st;
+    if (grad_gamma != nullptr || grad_beta != nullptr)
+      launch_colsum<true>(grad_out, x, means, rstds, grad_gamma, grad_beta, b, f, 0,
+                          f % 4 == 0 && al(grad_out, 16) && al(x, 16), stream);
+    if (grad_bias != nullptr)
+      launch_colsum<false>(grad_x, nullptr, nullptr, nullptr, grad_bias, nullptr, b, f, 0,
+                           f % 4 == 0 && al(grad_x, 16), stream);
+    return launched(fn);
+  }
+  const int planes = grad_bias != nullptr ? 3 : 2;
+  const size_t need = (size_t)((batch + 3) / 4) * planes * features * sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need || !al(workspace, 4))
+    return record_error(DFATTN_ERR_WORKSPACE, std::string(fn) + ": workspace must be non-null, 4-byte aligned and hold " +
+                                                  std::to_string(need) + " bytes");
+  float *partial = static_cast<float *>(workspace);
+  switch ((f / 4 + 63) / 64) {
+    case 1: launch_ln_fused_v<1>(grad_out, x, gamma, means, rstds, residual, grad_x, partial, planes, b, f, stream); break;
+    case 2: launch_ln_fused_v<2>(grad_out, x, gamma, means, rstds, residual, grad_x, partial, planes, b, f, stream); break;
+    case 3: launch_ln_fused_v<3>(grad_out, x, gamma, means, rstds, residual, grad_x, partial, planes, b, f, stream); break;
+    default: launch_ln_fused_v<4>(grad_out, x, gamma, means, rstds, residual, grad_x, partial, planes, b, f, stream); break;
+  }
+  if (int st = launched(fn); st != DFATTN_OK) return st;
+  hipLaunchKernelGGL(colsum_partials_kernel, dim3((planes * f + 15) / 16), dim3(256), 0, stream, partial,
+                     (b + 3) / 4, planes, f, grad_gamma, grad_beta, grad_bias);
+  return launched(fn);
 }
 
 extern "C" int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream) {

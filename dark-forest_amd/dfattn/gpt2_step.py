@@ -325,6 +325,8 @@ class _NativeEngine:
         if self.packed:
             buf("dqkv", 3, S, d)
         buf("dh", S, F)
+        # partial column sums of the fused LayerNorm backward
+        buf("ln_ws", (_ops.layer_norm_backward_fused_workspace_bytes(S, d) + 3) // 4)
         buf("da", S, F)
         offsets, n = {}, 0
         for name, shape in plan:
@@ -422,11 +424,12 @@ class _NativeEngine:
             _ops._dev_ptr(x), _ops._dev_ptr(g), _ops._dev_ptr(b), _ops._dev_ptr(out), _ops._dev_ptr(stats[0]),
             _ops._dev_ptr(stats[1]), rows, f, _ops._stream_ptr()))
 
-    @staticmethod
-    def _ln_backward(dy, x, g, b, stats, dx, residual=None):
+    def _ln_backward(self, dy, x, g, b, stats, dx, residual=None, bias=None):
         """dx = LayerNorm's input gradient (+ residual, a residual connection's gradient); gamma's
-        and beta's gradients written into their arena views."""
-        _ops.layer_norm_backward_residual_into(dy, x, g, stats, residual, dx, g.grad, b.grad)
+        and beta's gradients written into their arena views, and with `bias`, the gradient of the
+        linear layer's bias whose output gradient dx is (its column sums), from the same read."""
+        _ops.layer_norm_backward_fused_into(dy, x, g, stats, residual, dx, g.grad, b.grad,
+                                            bias.grad if bias is not None else None, self.b["ln_ws"])
 
     def _set_batch(self, tokens, targets):
         if tokens.shape[0] != self.m.seq_len or targets.shape[0] != self.m.seq_len:
@@ -512,23 +515,25 @@ class _NativeEngine:
         m, b, ex = self.m, self.b, self.exact_sites
         L = m.n_layers
         g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
-        self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g)
+        # Each LayerNorm backward also writes the bias gradient of the linear layer below it in the
+        # backward order (b2, or bo), the column sums of the residual-stream gradient it produces.
+        self._ln_backward(b["dlnf"], b[f"x{L}"], m.ln_f_g, m.ln_f_b, b["stf"], g,
+                          bias=m.layers[L - 1]["b2"] if L else None)
         for l in reversed(range(L)):
             lw = m.layers[l]
             # MLP: g is d(x_in[l+1]) = d(mlp out) = d(x_mid) through the residual
             self._linear_backward(b[f"a{l}"], lw["w2"], g, b["da"], ex["fc2_dx"], ex["fc2_dw"])
-            self._bias_grad(g, lw["b2"])
             _ops._check(_ops.ops_lib().dfgpt2_gelu_backward(_ops._dev_ptr(b["da"]), _ops._dev_ptr(b[f"h{l}"]),
                                                             _ops._dev_ptr(b["dh"]), b["dh"].numel(),
                                                             _ops._stream_ptr()))
             self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], ex["fc1_dx"], ex["fc1_dw"])
             self._bias_grad(b["dh"], lw["b1"])
             # d(x_mid) = g + LayerNorm 2's gradient
-            self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other, residual=g)
+            self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other, residual=g,
+                              bias=lw["bo"])
             g, other = other, g
             # attention: output projection, the fused attention backward, the Q/K/V projections
             self._linear_backward(b[f"att{l}"], lw["wo"], g, b["datt"], ex["wo_dx"], ex["wo_dw"])
-            self._bias_grad(g, lw["bo"])
             # dq | dk | dv side by side ([S, 3d]) for the fused projection's backward
             wide = b["wide"]
             grads = b["dqkv"].unbind(0) if self.packed else wide.split(m.d_model, dim=1)
@@ -538,7 +543,8 @@ class _NativeEngine:
             self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], ex["qkv_dx"], ex["qkv_dw"])
             self._bias_grad(wide, self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
-            self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other, residual=g)
+            self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other, residual=g,
+                              bias=m.layers[l - 1]["b2"] if l else None)
             g, other = other, g
         # embeddings (static_gpt2.rs:1559-1574): the token rows, and positions 0..S-1
         _ops.embedding_backward(self.ids, g, m.tok_emb.grad)

@@ -48,6 +48,8 @@ SYMBOLS = {
     "dfgpt2_add_layernorm_forward": (_I, [_P] * 8 + [_U32, _U32, _P]),
     "dfgpt2_layernorm_backward_residual": (_I, [_P] * 9 + [_U32, _U32, _P]),
     "dfgpt2_bias_gelu_forward": (_I, [_P] * 3 + [_U32, _U32, _P]),
+    "dfgpt2_layernorm_backward_fused_workspace_bytes": (_SZ, [_U32, _U32]),
+    "dfgpt2_layernorm_backward_fused": (_I, [_P] * 11 + [_SZ, _U32, _U32, _P]),
 }
 
 _typed = None
@@ -112,6 +114,23 @@ def layer_norm_backward_residual_into(grad_out, x, gamma, stats, residual, grad_
     _check(ops_lib().dfgpt2_layernorm_backward_residual(
         _dev_ptr(grad_out), _dev_ptr(x), _dev_ptr(gamma), _dev_ptr(stats[0]), _dev_ptr(stats[1]), res,
         _dev_ptr(grad_x), _dev_ptr(grad_gamma), _dev_ptr(grad_beta), rows, f, _stream_ptr()))
+
+
+def layer_norm_backward_fused_workspace_bytes(rows, features):
+    return int(ops_lib().dfgpt2_layernorm_backward_fused_workspace_bytes(rows, features))
+
+
+def layer_norm_backward_fused_into(grad_out, x, gamma, stats, residual, grad_x, grad_gamma, grad_beta, grad_bias,
+                                   workspace):
+    """dfgpt2_layernorm_backward_fused: layer_norm_backward_residual_into, plus grad_bias (unless None)
+    = the column sums of grad_x, with the rows read once; workspace: a float32 device tensor of at
+    least layer_norm_backward_fused_workspace_bytes(rows, features) bytes."""
+    rows, f = _rows_cols(x)
+    opt = lambda t: _dev_ptr(t) if t is not None else None
+    _check(ops_lib().dfgpt2_layernorm_backward_fused(
+        _dev_ptr(grad_out), _dev_ptr(x), opt(gamma), _dev_ptr(stats[0]), _dev_ptr(stats[1]), opt(residual),
+        _dev_ptr(grad_x), opt(grad_gamma), opt(grad_beta), opt(grad_bias), _dev_ptr(workspace),
+        workspace.numel() * workspace.element_size(), rows, f, _stream_ptr()))
 
 
 def bias_gelu_forward_into(h, bias, out):

@@ -106,6 +106,21 @@ int dfgpt2_layernorm_backward_residual(const float *grad_out, const float *x, co
                                        const float *means, const float *rstds, const float *residual,
                                        float *grad_x, float *grad_gamma, float *grad_beta, uint32_t batch,
                                        uint32_t features, hipStream_t stream);
+/* dfgpt2_layernorm_backward_residual, plus grad_bias[c] = sum over rows of grad_x[r, c] (the
+ * bias gradient of the linear layer whose output gradient grad_x is; NULL: not computed), with
+ * the rows read once: grad_x and each workgroup's partial column sums in one launch, then a
+ * fixed-order sum of the partials. grad_gamma, grad_beta and grad_bias are WRITTEN. The
+ * workspace (dfgpt2_layernorm_backward_fused_workspace_bytes, 4-byte aligned) holds the partial
+ * sums; nothing in it needs clearing. Reproducible bit for bit; the sums' order differs from the
+ * separate calls', so their last bits may too. Reference counterpart: separate launches, the
+ * engine's LayerNorm backwards (static_gpt2.rs:1427, 1474, 1543) and the bias gradients of b2
+ * and bo that the next linear backwards compute from their results (1451, 1490).            */
+size_t dfgpt2_layernorm_backward_fused_workspace_bytes(uint32_t batch, uint32_t features);
+int dfgpt2_layernorm_backward_fused(const float *grad_out, const float *x, const float *gamma,
+                                    const float *means, const float *rstds, const float *residual,
+                                    float *grad_x, float *grad_gamma, float *grad_beta, float *grad_bias,
+                                    void *workspace, size_t workspace_bytes, uint32_t batch,
+                                    uint32_t features, hipStream_t stream);
 /* h[r, c] += bias[c] in place (the GELU input the backward needs), out = gelu(h); [rows, cols];
  * out must not overlap h.                                                                      */
 int dfgpt2_bias_gelu_forward(float *h, const float *bias, float *out, uint32_t rows, uint32_t cols,

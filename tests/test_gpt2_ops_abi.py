@@ -12,7 +12,7 @@ from test_abi import declared_functions
 
 HEADER = os.path.join(ROOT, "include", "dfgpt2.h")
 # dfattn_status codes (include/dfattn.h)
-OK, ERR_NULL, ERR_MISALIGNED, ERR_SHAPE, ERR_OVERFLOW = dfattn.DFATTN_OK, -1, -2, -3, -5
+OK, ERR_NULL, ERR_MISALIGNED, ERR_SHAPE, ERR_OVERFLOW, ERR_WORKSPACE = dfattn.DFATTN_OK, -1, -2, -3, -5, -6
 
 
 def test_every_declared_symbol_is_exported_and_typed():
@@ -78,6 +78,21 @@ ODD = ctypes.c_void_p(0x1002)
     ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 4, 0, None), ERR_SHAPE),
     ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 2**31, 8, None), ERR_OVERFLOW),
     ("dfgpt2_bias_gelu_forward", (None, None, None, 0, 8, None), OK),
+    # fused LayerNorm backward: (grad_out, x, gamma, means, rstds, residual, grad_x, grad_gamma,
+    # grad_beta, grad_bias, workspace, workspace_bytes, batch, features, stream)
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, None, BUF, None, None, BUF, 1 << 20, 4, 8,
+                                         None), ERR_NULL),
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, ODD, BUF, BUF, None, None, BUF, 1 << 20, 4, 8,
+                                         None), ERR_MISALIGNED),
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, BUF, BUF, None, None, BUF, 1 << 20, 4, 0,
+                                         None), ERR_SHAPE),
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, BUF, BUF, None, None, None, 1 << 20, 4, 8,
+                                         None), ERR_WORKSPACE),
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, BUF, BUF, BUF, None, BUF, 63, 4, 8, None),
+     ERR_WORKSPACE),  # two planes of 8 sums for one workgroup need 64 bytes
+    ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, BUF, None, None, BUF, BUF, 95, 4, 8, None),
+     ERR_WORKSPACE),  # with the bias plane, 96
+    ("dfgpt2_layernorm_backward_fused", (None,) * 10 + (None, 0, 0, 8, None), OK),
 ])
 def test_argument_errors_are_caught_on_the_host(fn, args, status):
     ops.ops_lib().dfattn_clear_error()
@@ -85,6 +100,14 @@ def test_argument_errors_are_caught_on_the_host(fn, args, status):
     if status != OK:
         assert ops.ops_lib().dfattn_last_error() == status
     ops.ops_lib().dfattn_clear_error()
+
+
+def test_fused_layernorm_backward_workspace_formula():
+    """Per workgroup of four rows, three planes (gamma, beta and bias terms) of features floats."""
+    lib = ops.ops_lib()
+    for rows, f in ((1024, 768), (1, 8), (5, 100), (4, 8)):
+        assert lib.dfgpt2_layernorm_backward_fused_workspace_bytes(rows, f) == (rows + 3) // 4 * 3 * f * 4
+    assert lib.dfgpt2_layernorm_backward_fused_workspace_bytes(0, 768) == 0
 
 
 def test_reference_launcher_records_error_for_darkforest_sync():

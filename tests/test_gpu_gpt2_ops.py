@@ -307,6 +307,46 @@ def test_add_layernorm_is_the_add_then_the_layernorm(device, rows, f):
     close(out, ref, 1e-5, 1e-5, "add+layernorm vs torch")
 
 
+@pytest.mark.parametrize("rows,f", LN_SHAPES + [(5, 100), (1030, 1024)])
+@pytest.mark.parametrize("residual,bias", [(True, True), (False, True), (True, False)])
+def test_fused_layernorm_backward_is_the_separate_calls(device, rows, f, residual, bias):
+    """dfgpt2_layernorm_backward_fused: grad_x bit for bit the separate dfgpt2_layernorm_backward_residual's,
+    the parameter gradients and grad_x's column sums (the next bias gradient) against float64 sums
+    of the same products, all three written over what their buffers held, bitwise reproducible;
+    the partial-sum workspace filled with NaN first (nothing in it is read before written)."""
+    import torch
+
+    say(f"fused layernorm backward rows={rows} f={f} residual={residual} bias={bias}")
+    g = torch.Generator(device="cpu").manual_seed(rows * 7 + f)
+    x, dy = torch.randn(rows, f, generator=g).to(device), torch.randn(rows, f, generator=g).to(device)
+    res = torch.randn(rows, f, generator=g).to(device) if residual else None
+    gamma, beta = torch.randn(f, generator=g).to(device), torch.randn(f, generator=g).to(device)
+    _, m, r = ops.layer_norm_forward(x, gamma, beta)
+    stats = torch.stack([m, r])
+    gx0 = torch.empty_like(x)
+    gg0, gb0 = torch.empty(f, device=device), torch.empty(f, device=device)
+    ops.layer_norm_backward_residual_into(dy, x, gamma, stats, res, gx0, gg0, gb0)
+    ws = torch.full((ops.layer_norm_backward_fused_workspace_bytes(rows, f) // 4,), float("nan"), device=device)
+    outs = []
+    for _ in range(2):
+        gx = torch.full_like(x, float("nan"))
+        gg, gb = torch.full((f,), 7.0, device=device), torch.full((f,), -3.0, device=device)
+        gbias = torch.full((f,), 5.0, device=device) if bias else None
+        ops.layer_norm_backward_fused_into(dy, x, gamma, stats, res, gx, gg, gb, gbias, ws)
+        torch.cuda.synchronize()
+        outs.append((gx, gg, gb, gbias))
+    gx, gg, gb, gbias = outs[0]
+    assert torch.equal(gx, gx0)
+    xh = (x.double() - m.double()[:, None]) * r.double()[:, None]
+    n = max(rows, 1) ** 0.5
+    close(gg.double(), (dy.double() * xh).sum(0), 0, 2e-5 * n, "grad gamma")
+    close(gb.double(), dy.double().sum(0), 0, 2e-5 * n, "grad beta")
+    if bias:
+        close(gbias.double(), gx0.double().sum(0), 0, 2e-5 * n * max(1.0, gx0.abs().max().item()), "grad bias")
+    for a, b2 in zip(outs[0], outs[1]):
+        assert a is None or torch.equal(a, b2)
+
+
 @pytest.mark.parametrize("rows,f", LN_SHAPES)
 def test_layernorm_backward_residual_adds_and_overwrites(device, rows, f):
     """dfgpt2_layernorm_backward_residual: grad_x is dfgpt2_layernorm_backward's plus the residual
