@@ -321,16 +321,16 @@ def summarize_trace(stats_csv):
 def _gpt2_kernel_class(name):
     """Category of a kernel of the GPT-2 step (for the per-step breakdown)."""
     low = name.lower()
+    ln = "LayerNorm fwd/bwd, with the b2/bo bias gradients (dfgpt2)"
     for key, label in (("cijk", "GEMM (hipBLASLt fp32)"), ("fwd_d64", "attention forward (dfattn)"),
-                       ("ln_fwd", "LayerNorm fwd/bwd (dfgpt2)"), ("ln_bwd", "LayerNorm fwd/bwd (dfgpt2)"),
-                       ("colsum_vec_kernel<true", "LayerNorm fwd/bwd (dfgpt2)"),
-                       ("colsum_generic_kernel<true", "LayerNorm fwd/bwd (dfgpt2)"),
-                       ("colsum", "bias gradients (dfgpt2)"), ("gelu_kernel", "GELU fwd/bwd (dfgpt2)"),
+                       ("ln_fwd", ln), ("ln_bwd", ln), ("colsum_partials", ln), ("colsum_vec_kernel<true", ln),
+                       ("colsum_generic_kernel<true", ln),
+                       ("colsum", "bias gradients of bqkv and b1 (dfgpt2)"), ("gelu_kernel", "GELU fwd/bwd (dfgpt2)"),
                        ("adamw_kernel", "AdamW (dfgpt2, one launch over the arena)"),
                        ("step_advance", "AdamW (dfgpt2, one launch over the arena)"),
                        ("bwd_main", "attention backward main (dfattn)"), ("bwd_pre", "attention backward phase 1 (dfattn)"),
                        ("fusedopti", "AdamW (fused)"),
-                       ("ce_row_kernel", "cross-entropy, chunked fused (dfgpt2)"),
+                       ("ce_row", "cross-entropy, chunked fused (dfgpt2)"),
                        ("sum_kernel", "cross-entropy, chunked fused (dfgpt2)"),
                        ("embed_fwd", "embedding fwd/bwd (dfgpt2)"), ("embed_bwd", "embedding fwd/bwd (dfgpt2)"),
                        ("softmax", "softmax / cross-entropy (torch)"), ("nll", "softmax / cross-entropy (torch)"),
