@@ -457,6 +457,40 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float *__restrict__ go,
   }
 }
 
+// The reference step's plain elementwise launchers (elementwise.cu:48-124,
+// 229-250), one fp32 operation per value: OP 0 c = a + b, 1 c = alpha * a,
+// 2 c = alpha, 3 c = a + b[column] (b a bias over rows of `cols` values).
+// Grid-stride over float4 groups when `vec` (every pointer 16-byte aligned
+// and, for the bias, cols % 4 == 0), value by value otherwise; c may be a.
+template <int OP>
+__global__ __launch_bounds__(256) void ew_kernel(const float *a, const float *__restrict__ b, float *c, float alpha,
+                                                 size_t n, int cols, int vec) {
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  auto op = [&](float x, float y) {
+    if constexpr (OP == 0 || OP == 3) return x + y;
+    else if constexpr (OP == 1) return alpha * x;
+    else return alpha;
+  };
+  size_t done = 0;
+  if (vec) {
+    const size_t n4 = n / 4;
+    const size_t c4 = (size_t)cols / 4;
+    for (size_t i = tid; i < n4; i += stride) {
+      const float4 x = OP == 2 ? splat4(0.f) : reinterpret_cast<const float4 *>(a)[i];
+      const float4 y = OP == 0   ? reinterpret_cast<const float4 *>(b)[i]
+                       : OP == 3 ? reinterpret_cast<const float4 *>(b)[i % c4]
+                                 : splat4(0.f);
+      reinterpret_cast<float4 *>(c)[i] = make_float4(op(x.x, y.x), op(x.y, y.y), op(x.z, y.z), op(x.w, y.w));
+    }
+    done = n4 * 4;
+  }
+  for (size_t i = done + tid; i < n; i += stride) {
+    const float x = OP == 2 ? 0.f : a[i];
+    const float y = OP == 0 ? b[i] : (OP == 3 ? b[i % (size_t)cols] : 0.f);
+    c[i] = op(x, y);
+  }
+}
+
 // h = h + bias (bias broadcast over rows of `cols` values, written back: the
 // backward's GELU input) and out = gelu(h), in one pass over [rows, cols].
 // vec: cols % 4 == 0 and 16-byte aligned tensors.
@@ -792,6 +826,29 @@ extern "C" int dfgpt2_layernorm_backward_fused(const float *grad_out, const floa
   return launched(fn);
 }
 
+namespace dfattn {
+namespace {
+template <int OP>
+void launch_ew(const float *a, const float *b, float *c, float alpha, size_t n, int cols, bool vec,
+               hipStream_t stream) {
+  hipLaunchKernelGGL(ew_kernel<OP>, dim3(elementwise_blocks(n)), dim3(256), 0, stream, a, b, c, alpha, n, cols,
+                     vec ? 1 : 0);
+}
+}  // namespace
+}  // namespace dfattn
+
+extern "C" int dfgpt2_add_bias(const float *input, const float *bias, float *out, uint32_t batch, uint32_t features,
+                               hipStream_t stream) {
+  const char *fn = "dfgpt2_add_bias";
+  if (int st = check_dims(fn, batch, features); st != DFATTN_OK) return st;
+  if (batch == 0) return DFATTN_OK;
+  if (int st = check_ptrs(fn, {input, bias, out}, {}); st != DFATTN_OK) return st;
+  const size_t n = (size_t)batch * features;
+  launch_ew<3>(input, bias, out, 0.f, n, (int)features, features % 4 == 0 && al(input, 16) && al(bias, 16) && al(out, 16),
+               stream);
+  return launched(fn);
+}
+
 extern "C" int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream) {
   const char *fn = "dfgpt2_gelu_forward";
   if (n == 0) return DFATTN_OK;
@@ -864,6 +921,49 @@ extern "C" void launch_layernorm_backward(const float *grad_out, const float *x,
                                           float *grad_beta, uint32_t batch, uint32_t features) {
   mark_pending(dfgpt2_layernorm_backward(grad_out, x, gamma, means, rstds, grad_x, grad_gamma, grad_beta, batch,
                                          features, nullptr));
+}
+
+// elementwise.cu:242 (null stream; out may be input).
+extern "C" void launch_add_bias(const float *input, const float *bias, float *out, uint32_t batch,
+                                uint32_t features) {
+  mark_pending(dfgpt2_add_bias(input, bias, out, batch, features, nullptr));
+}
+
+// elementwise.cu:62, 91, 119: fill, add and scale of n values (null stream).
+extern "C" void launch_fill(float *c, float val, uint32_t n) {
+  int st = DFATTN_OK;
+  if (n > 0) {
+    st = check_ptrs("launch_fill", {c}, {});
+    if (st == DFATTN_OK) {
+      launch_ew<2>(nullptr, nullptr, c, val, n, 1, al(c, 16), nullptr);
+      st = launched("launch_fill");
+    }
+  }
+  mark_pending(st);
+}
+
+extern "C" void launch_add(const float *a, const float *b, float *c, uint32_t n) {
+  int st = DFATTN_OK;
+  if (n > 0) {
+    st = check_ptrs("launch_add", {a, b, c}, {});
+    if (st == DFATTN_OK) {
+      launch_ew<0>(a, b, c, 0.f, n, 1, al(a, 16) && al(b, 16) && al(c, 16), nullptr);
+      st = launched("launch_add");
+    }
+  }
+  mark_pending(st);
+}
+
+extern "C" void launch_scale(const float *a, float alpha, float *c, uint32_t n) {
+  int st = DFATTN_OK;
+  if (n > 0) {
+    st = check_ptrs("launch_scale", {a, c}, {});
+    if (st == DFATTN_OK) {
+      launch_ew<1>(a, nullptr, c, alpha, n, 1, al(a, 16) && al(c, 16), nullptr);
+      st = launched("launch_scale");
+    }
+  }
+  mark_pending(st);
 }
 
 extern "C" void launch_gelu(const float *x, float *out, uint32_t n) {

@@ -391,7 +391,8 @@ class _NativeEngine:
 
     def _linear(self, x, w, b, out, exact=True):
         """out = x W^T + b (static_gpt2.rs linear_into; hipBLASLt). exact: one GEMM with the bias in
-        its epilogue on the exact fp32 path; otherwise the fast-path GEMM, then the bias added."""
+        its epilogue on the exact fp32 path; otherwise the fast-path GEMM, then the bias added in
+        place (dfgpt2_add_bias)."""
         torch = _torch()
         if exact:
             self._exact(True)
@@ -399,7 +400,7 @@ class _NativeEngine:
             self._exact(False)
         else:
             torch.mm(x, w.t(), out=out)
-            out.add_(b)
+            _ops.add_bias_into(out, b)
 
     def _linear_backward(self, x, w, dy, dx, exact_dx=False, exact_dw=False):
         """dx = dy W and W's gradient dy^T x, into the arena gradient view (static_gpt2.rs

@@ -49,6 +49,11 @@ SYMBOLS = {
     "dfgpt2_layernorm_backward_residual": (_I, [_P] * 9 + [_U32, _U32, _P]),
     "dfgpt2_bias_gelu_forward": (_I, [_P] * 3 + [_U32, _U32, _P]),
     "dfgpt2_layernorm_backward_fused_workspace_bytes": (_SZ, [_U32, _U32]),
+    "launch_add_bias": (None, [_P] * 3 + [_U32, _U32]),
+    "launch_fill": (None, [_P, _F, _U32]),
+    "launch_add": (None, [_P] * 3 + [_U32]),
+    "launch_scale": (None, [_P, _F, _P, _U32]),
+    "dfgpt2_add_bias": (_I, [_P] * 3 + [_U32, _U32, _P]),
     "dfgpt2_layernorm_backward_fused": (_I, [_P] * 11 + [_SZ, _U32, _U32, _P]),
 }
 
@@ -131,6 +136,14 @@ def layer_norm_backward_fused_into(grad_out, x, gamma, stats, residual, grad_x, 
         _dev_ptr(grad_out), _dev_ptr(x), opt(gamma), _dev_ptr(stats[0]), _dev_ptr(stats[1]), opt(residual),
         _dev_ptr(grad_x), opt(grad_gamma), opt(grad_beta), opt(grad_bias), _dev_ptr(workspace),
         workspace.numel() * workspace.element_size(), rows, f, _stream_ptr()))
+
+
+def add_bias_into(x, bias, out=None):
+    """dfgpt2_add_bias: out = x + bias per row (out=None: in place)."""
+    rows, cols = _rows_cols(x)
+    out = x if out is None else out
+    _check(ops_lib().dfgpt2_add_bias(_dev_ptr(x), _dev_ptr(bias), _dev_ptr(out), rows, cols, _stream_ptr()))
+    return out
 
 
 def bias_gelu_forward_into(h, bias, out):

@@ -1,7 +1,7 @@
 /* dfgpt2.h — C ABI of the GPT-2 step's non-attention kernels in libdfattn.so (gfx950).
  *
  * The reference engine's training step (darkforest-core/src/engine/static_gpt2.rs:1375-1696)
- * calls these CUDA launchers around its attention; the six reference symbols below keep their
+ * calls these CUDA launchers around its attention; the reference symbols below keep their
  * signatures and semantics (null stream, void return, argument errors reported by
  * darkforest_sync, declared in dfattn.h). The dfgpt2_* entry points are the same kernels on an
  * explicit stream with a dfattn_status return. Every reduction adds in a fixed order (no
@@ -29,6 +29,14 @@ void launch_layernorm_backward(const float *grad_out, const float *x, const floa
 /* elementwise.cu:195, 217: tanh GELU, 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))). */
 void launch_gelu(const float *x, float *out, uint32_t n);
 void launch_gelu_backward(const float *grad_out, const float *x, float *grad_x, uint32_t n);
+/* elementwise.cu:242: out[r, c] = input[r, c] + bias[c] over [batch, features] (out may be input),
+ * the bias add after each linear layer's GEMM (lib.rs linear_into). elementwise.cu:62, 91, 119:
+ * c = val, c = a + b, c = alpha * a over n values (residual adds and gradient scaling of the
+ * step, lib.rs add_into / scale). One fp32 operation per value, as the reference. */
+void launch_add_bias(const float *input, const float *bias, float *out, uint32_t batch, uint32_t features);
+void launch_fill(float *c, float val, uint32_t n);
+void launch_add(const float *a, const float *b, float *c, uint32_t n);
+void launch_scale(const float *a, float alpha, float *c, uint32_t n);
 /* matmul.cu:240: grad_bias[j] = sum over rows of grad_out[row, j] (overwritten). */
 void launch_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch, uint32_t out_features);
 /* matmul.cu:341: m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;
@@ -62,6 +70,9 @@ int dfgpt2_layernorm_backward(const float *grad_out, const float *x, const float
                               uint32_t batch, uint32_t features, hipStream_t stream);
 int dfgpt2_gelu_forward(const float *x, float *out, size_t n, hipStream_t stream);
 int dfgpt2_gelu_backward(const float *grad_out, const float *x, float *grad_x, size_t n, hipStream_t stream);
+/* launch_add_bias on a stream. */
+int dfgpt2_add_bias(const float *input, const float *bias, float *out, uint32_t batch, uint32_t features,
+                    hipStream_t stream);
 /* accumulate != 0: grad_bias += column sums (else overwritten). */
 int dfgpt2_linear_grad_bias(const float *grad_out, float *grad_bias, uint32_t batch, uint32_t out_features,
                             int accumulate, hipStream_t stream);

@@ -78,6 +78,11 @@ ODD = ctypes.c_void_p(0x1002)
     ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 4, 0, None), ERR_SHAPE),
     ("dfgpt2_bias_gelu_forward", (BUF, BUF, BUF, 2**31, 8, None), ERR_OVERFLOW),
     ("dfgpt2_bias_gelu_forward", (None, None, None, 0, 8, None), OK),
+    ("dfgpt2_add_bias", (BUF, None, BUF, 4, 8, None), ERR_NULL),
+    ("dfgpt2_add_bias", (BUF, BUF, ODD, 4, 8, None), ERR_MISALIGNED),
+    ("dfgpt2_add_bias", (BUF, BUF, BUF, 4, 0, None), ERR_SHAPE),
+    ("dfgpt2_add_bias", (BUF, BUF, BUF, 2**31, 8, None), ERR_OVERFLOW),
+    ("dfgpt2_add_bias", (None, None, None, 0, 8, None), OK),
     # fused LayerNorm backward: (grad_out, x, gamma, means, rstds, residual, grad_x, grad_gamma,
     # grad_beta, grad_bias, workspace, workspace_bytes, batch, features, stream)
     ("dfgpt2_layernorm_backward_fused", (BUF, BUF, None, BUF, BUF, None, None, BUF, None, None, BUF, 1 << 20, 4, 8,
@@ -129,3 +134,18 @@ def test_reference_launcher_records_error_for_darkforest_sync():
     assert lib.dfattn_last_error() == ERR_NULL
     assert "dfgpt2_embedding_backward" in lib.dfattn_last_error_message().decode()
     lib.dfattn_clear_error()
+    for call, name in ((lambda: lib.launch_add_bias(BUF, None, BUF, 4, 8), "dfgpt2_add_bias"),
+                       (lambda: lib.launch_add(BUF, None, BUF, 16), "launch_add"),
+                       (lambda: lib.launch_scale(None, 2.0, BUF, 16), "launch_scale"),
+                       (lambda: lib.launch_fill(None, 1.0, 16), "launch_fill")):
+        call()
+        assert lib.dfattn_last_error() == ERR_NULL
+        assert name in lib.dfattn_last_error_message().decode()
+        lib.dfattn_clear_error()
+    lib.launch_add(ODD, BUF, BUF, 16)
+    assert lib.dfattn_last_error() == ERR_MISALIGNED
+    lib.dfattn_clear_error()
+    for call in (lambda: lib.launch_add(None, None, None, 0), lambda: lib.launch_scale(None, 2.0, None, 0),
+                 lambda: lib.launch_fill(None, 1.0, 0), lambda: lib.launch_add_bias(None, None, None, 0, 8)):
+        call()  # nothing to do: no error, nothing launched
+        assert lib.dfattn_last_error() == OK

@@ -307,6 +307,40 @@ def test_add_layernorm_is_the_add_then_the_layernorm(device, rows, f):
     close(out, ref, 1e-5, 1e-5, "add+layernorm vs torch")
 
 
+@pytest.mark.parametrize("rows,cols", [(1024, 2304), (7, 13), (3, 4)])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_elementwise_launchers_are_the_torch_ops(device, rows, cols, offset):
+    """dfgpt2_add_bias (out of place and in place) and the reference's launch_add_bias, launch_add,
+    launch_scale and launch_fill: one fp32 operation per value, so bit for bit torch's; offset 1
+    starts every tensor one float into its buffer (not 16-byte aligned: the value-by-value path)."""
+    import torch
+
+    say(f"elementwise rows={rows} cols={cols} offset={offset}")
+    g = torch.Generator(device="cpu").manual_seed(rows + cols + offset)
+    n = rows * cols
+    buf = lambda: torch.randn(n + 1, generator=g).to(device)
+    x, y, bias = buf()[offset:offset + n].view(rows, cols), buf()[offset:offset + n], buf()[offset:offset + cols]
+    out = torch.full_like(x, float("nan"))
+    ops.add_bias_into(x, bias, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, x + bias)
+    inplace = x.clone()
+    ops.add_bias_into(inplace, bias)
+    lib = ops.ops_lib()
+    ref_out = torch.full_like(x, float("nan"))
+    lib.launch_add_bias(P(x), P(bias), P(ref_out), rows, cols)
+    xf = x.reshape(-1)
+    c = torch.full_like(y, float("nan"))
+    lib.launch_add(P(xf), P(y), P(c), n)
+    s = torch.full_like(y, float("nan"))
+    lib.launch_scale(P(xf), 0.37, P(s), n)
+    f = torch.full_like(y, float("nan"))
+    lib.launch_fill(P(f), -2.5, n)
+    dfattn.darkforest_sync()
+    assert torch.equal(inplace, x + bias) and torch.equal(ref_out, x + bias)
+    assert torch.equal(c, xf + y) and torch.equal(s, 0.37 * xf) and bool((f == -2.5).all())
+
+
 @pytest.mark.parametrize("rows,f", LN_SHAPES + [(5, 100), (1030, 1024)])
 @pytest.mark.parametrize("residual,bias", [(True, True), (False, True), (True, False)])
 def test_fused_layernorm_backward_is_the_separate_calls(device, rows, f, residual, bias):
