@@ -325,7 +325,7 @@ def _gpt2_kernel_class(name):
     for key, label in (("cijk", "GEMM (hipBLASLt fp32)"), ("fwd_d64", "attention forward (dfattn)"),
                        ("ln_fwd", ln), ("ln_bwd", ln), ("colsum_partials", ln), ("colsum_vec_kernel<true", ln),
                        ("colsum_generic_kernel<true", ln),
-                       ("colsum", "bias gradients of bqkv and b1 (dfgpt2)"), ("gelu_kernel", "GELU fwd/bwd (dfgpt2)"),
+                       ("colsum", "bias gradients of bqkv and b1 (dfgpt2)"), ("ew_kernel<3>", "Q/K/V bias add (dfgpt2)"), ("gelu_kernel", "GELU fwd/bwd (dfgpt2)"),
                        ("adamw_kernel", "AdamW (dfgpt2, one launch over the arena)"),
                        ("step_advance", "AdamW (dfgpt2, one launch over the arena)"),
                        ("bwd_main", "attention backward main (dfattn)"), ("bwd_pre", "attention backward phase 1 (dfattn)"),
