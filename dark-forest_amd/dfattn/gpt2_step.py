@@ -343,6 +343,10 @@ class _NativeEngine:
         self.ids, self.tgt, self.pos = ints[:S], ints[w:w + S], ints[2 * w:2 * w + S]
         self.pos.copy_(torch.arange(S, dtype=torch.int32, device=dev))
         self.ctx = [AttentionContext(H, S, d // H, reuse_forward=True) for _ in range(L)]
+        # In a captured step the backward's weight-gradient GEMMs run on this stream, beside the
+        # input-gradient ones (eager dispatch of the cross-stream waits costs more than it gains).
+        self.side = torch.cuda.Stream(device=dev) if torch.device(dev).type == "cuda" else None
+        self._overlap = False
         self.scale = (d / H) ** -0.5
         # Views of each layer's Q, K, V weights (and biases, and their gradients) as one [3d, d]
         # ([3d]) tensor: they are adjacent in the parameter arena.
@@ -406,10 +410,20 @@ class _NativeEngine:
         """dx = dy W and W's gradient dy^T x, into the arena gradient view (static_gpt2.rs
         linear_backward_into); exact_dx / exact_dw: that product on the exact fp32 GEMM path."""
         torch = _torch()
+        if self._overlap:
+            # The previous weight gradient has finished before this one starts (and before the main
+            # stream goes on to overwrite what that one read); this one starts after dy is written.
+            main = torch.cuda.current_stream()
+            main.wait_stream(self.side)
+            self.side.wait_stream(main)
         self._exact(exact_dx)
         torch.mm(dy, w, out=dx)
         self._exact(exact_dw)
-        torch.mm(dy.t(), x, out=w.grad)
+        if self._overlap:
+            with torch.cuda.stream(self.side):
+                torch.mm(dy.t(), x, out=w.grad)
+        else:
+            torch.mm(dy.t(), x, out=w.grad)
         self._exact(False)
 
     @staticmethod
@@ -514,6 +528,9 @@ class _NativeEngine:
     # ---------------------------------------------------------------- backward (static_gpt2.rs:1424-1575)
     def _backward(self):
         m, b, ex = self.m, self.b, self.exact_sites
+        self._overlap = self.side is not None and _torch().cuda.is_current_stream_capturing()
+        if self._overlap:
+            self.side.wait_stream(_torch().cuda.current_stream())
         L = m.n_layers
         g, other = b["g0"], b["g1"]  # gradient of the residual stream, and the next layer's
         # Each LayerNorm backward also writes the bias gradient of the linear layer below it in the
@@ -550,6 +567,8 @@ class _NativeEngine:
         # embeddings (static_gpt2.rs:1559-1574): the token rows, and positions 0..S-1
         _ops.embedding_backward(self.ids, g, m.tok_emb.grad)
         _ops.embedding_backward(self.pos, g, m.pos_emb.grad)
+        if self._overlap:
+            _torch().cuda.current_stream().wait_stream(self.side)  # the last weight gradient
 
     def _zero_accumulated_grads(self):
         """Only the embedding gradients are accumulated (the embedding backward adds into them);
