@@ -406,9 +406,10 @@ class _NativeEngine:
             torch.mm(x, w.t(), out=out)
             _ops.add_bias_into(out, b)
 
-    def _linear_backward(self, x, w, dy, dx, exact_dx=False, exact_dw=False):
+    def _linear_backward(self, x, w, dy, dx, exact_dx=False, exact_dw=False, bias=None):
         """dx = dy W and W's gradient dy^T x, into the arena gradient view (static_gpt2.rs
-        linear_backward_into); exact_dx / exact_dw: that product on the exact fp32 GEMM path."""
+        linear_backward_into); exact_dx / exact_dw: that product on the exact fp32 GEMM path;
+        bias: its gradient too (the column sums of dy), beside W's."""
         torch = _torch()
         if self._overlap:
             # The previous weight gradient has finished before this one starts (and before the main
@@ -422,8 +423,12 @@ class _NativeEngine:
         if self._overlap:
             with torch.cuda.stream(self.side):
                 torch.mm(dy.t(), x, out=w.grad)
+                if bias is not None:
+                    self._bias_grad(dy, bias)
         else:
             torch.mm(dy.t(), x, out=w.grad)
+            if bias is not None:
+                self._bias_grad(dy, bias)
         self._exact(False)
 
     @staticmethod
@@ -544,8 +549,7 @@ class _NativeEngine:
             _ops._check(_ops.ops_lib().dfgpt2_gelu_backward(_ops._dev_ptr(b["da"]), _ops._dev_ptr(b[f"h{l}"]),
                                                             _ops._dev_ptr(b["dh"]), b["dh"].numel(),
                                                             _ops._stream_ptr()))
-            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], ex["fc1_dx"], ex["fc1_dw"])
-            self._bias_grad(b["dh"], lw["b1"])
+            self._linear_backward(b[f"ln2{l}"], lw["w1"], b["dh"], b["dln"], ex["fc1_dx"], ex["fc1_dw"], lw["b1"])
             # d(x_mid) = g + LayerNorm 2's gradient
             self._ln_backward(b["dln"], b[f"xmid{l}"], lw["ln2_g"], lw["ln2_b"], b[f"st2{l}"], other, residual=g,
                               bias=lw["bo"])
@@ -558,8 +562,8 @@ class _NativeEngine:
             self.ctx[l].backward_device_into(*self._qkv(l), b["datt"], self.scale, True, *grads)
             if self.packed:
                 wide.view(m.seq_len, 3, -1).copy_(b["dqkv"].transpose(0, 1))
-            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], ex["qkv_dx"], ex["qkv_dw"])
-            self._bias_grad(wide, self.bqkv[l])
+            self._linear_backward(b[f"ln1{l}"], self.wqkv[l], wide, b["dln"], ex["qkv_dx"], ex["qkv_dw"],
+                                  self.bqkv[l])
             # d(x_in[l]) = d(x_mid) + LayerNorm 1's gradient
             self._ln_backward(b["dln"], b[f"x{l}"], lw["ln1_g"], lw["ln1_b"], b[f"st1{l}"], other, residual=g,
                               bias=m.layers[l - 1]["b2"] if l else None)
