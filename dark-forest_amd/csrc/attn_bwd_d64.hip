@@ -115,7 +115,8 @@ inline WsLayout ws_layout(int H, int S) {
 }
 
 // Phase 1: 64 rows of one head per workgroup (256 threads; thread t owns row
-// t/4, columns 16*(t%4) .. +15 of each tensor). The block's dO scale sigma_b
+// t/4, columns 4*(t%4) + 16*i .. +3 for i = 0..3 of each tensor, so that the
+// four threads of a row read one contiguous 64 bytes per load). The block's dO scale sigma_b
 // comes from the block's own max |dO|, so blocks are independent and phase 1
 // is one launch. Delta is summed from the same rounded sigma_b * dO that the
 // main kernel's dP products use, so the rows of dS = P * (dP - Delta) sum to
@@ -133,23 +134,23 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
   const int head = blockIdx.y;
   const int row = blockIdx.x * kPreRows + (tid >> 2);
   const bool ok = row < S;
-  const size_t src = ok ? (size_t)row * H * kD + (size_t)head * kD + (tid & 3) * 16 : 0;
-  const size_t src_in = ok ? (size_t)row * ldi + (size_t)head * kD + (tid & 3) * 16 : 0;  // Q, K, V
-  const size_t dst = ((size_t)head * S + row) * kD + (tid & 3) * 16;
+  const size_t src = ok ? (size_t)row * H * kD + (size_t)head * kD + (tid & 3) * 4 : 0;
+  const size_t src_in = ok ? (size_t)row * ldi + (size_t)head * kD + (tid & 3) * 4 : 0;  // Q, K, V
+  const size_t dst = ((size_t)head * S + row) * kD + (tid & 3) * 4;
   const size_t r = (size_t)head * S + row;
   // Every load first.
   float4 g[4], o[4], x[3][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    g[i] = load4_or_zero(dO + src + 4 * i, ok);
-    o[i] = load4_or_zero(O + src + 4 * i, ok);
+    g[i] = load4_or_zero(dO + src + 16 * i, ok);
+    o[i] = load4_or_zero(O + src + 16 * i, ok);
   }
   const float *in[3] = {Q, K, V};
   if (convert_qkv) {
 #pragma unroll
     for (int t = 0; t < 3; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src_in + 4 * i, ok);
+      for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src_in + 16 * i, ok);
   }
   const float l = ok ? lse[r] : 0.f;
   float mx = 0.f;
@@ -180,27 +181,15 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     deltan[r] = -acc;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    *reinterpret_cast<half8_t *>(do16 + dst + 8 * i) = half8_t{h[2 * i][0], h[2 * i][1], h[2 * i][2], h[2 * i][3],
-                                                               h[2 * i + 1][0], h[2 * i + 1][1], h[2 * i + 1][2],
-                                                               h[2 * i + 1][3]};
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<half4_t *>(do16 + dst + 16 * i) = h[i];
   if (!convert_qkv) return;
   half_t *out[3] = {q16, k16, v16};
 #pragma unroll
   for (int t = 0; t < 3; ++t)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      half4_t lo, hi;
-      if (t == 0) {
-        lo = round_scaled4(x[t][2 * i], c2);
-        hi = round_scaled4(x[t][2 * i + 1], c2);
-      } else {
-        lo = to_half4(x[t][2 * i]);
-        hi = to_half4(x[t][2 * i + 1]);
-      }
-      *reinterpret_cast<half8_t *>(out[t] + dst + 8 * i) =
-          half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<half4_t *>(out[t] + dst + 16 * i) =
+          t == 0 ? round_scaled4(x[t][i], c2) : to_half4(x[t][i]);
 }
 
 // Relative cost of one step of each item kind (measured at C2: a dK/dV step,
