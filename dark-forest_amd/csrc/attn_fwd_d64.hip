@@ -46,12 +46,13 @@ constexpr int kVRingBytes = kStages * kTileBytes;
 constexpr int kF4 = kBN * kD / 4 / kThreads;  // float4 of K (and of V) per thread per tile
 static_assert(kF4 * kThreads * 4 == kBN * kD, "tile split");
 static_assert(kThreads * 8 == kTile, "one half8 per thread clears a tile");
-// Merge buffer: per partner wave, 32 output registers + max + sum, lane-major.
-constexpr int kMergeRegs = 34;
+// Merge buffer: per wave, the 16 output registers it hands to its partner +
+// max + sum, lane-major.
+constexpr int kMergeRegs = 18;
 constexpr float kRescale = 8.f;  // log2 headroom of the softmax reference point
 constexpr float kRescaleSum = 256.f;  // 2^kRescale
 constexpr int kRingBytes = 2 * kStages * kTileBytes;
-constexpr int kMergeBytes = 4 * kMergeRegs * 64 * 4;
+constexpr int kMergeBytes = kWaves * kMergeRegs * 64 * 4;
 // After the rings: the workgroup's 128 Q rows as a [128][64] fp16 tile (c2 Q),
 // staged once with coalesced loads; each wave reads its fragments from it.
 constexpr int kQTileBytes = kBM * kD * 2;
@@ -548,46 +549,42 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     }
   }
 
-  // Merge the key halves: wave qg+4 hands (o, m, l) to wave qg through LDS.
-  float *mbuf = reinterpret_cast<float *>(lds_raw) + (size_t)qg * kMergeRegs * 64;
-  if (kh == 1) {
+  // Merge the key halves: waves qg (kh 0) and qg+4 (kh 1) swap halves of their
+  // output through LDS, each handing over the 32-column block the other
+  // finishes (with its m and l); wave kh then merges and stores columns
+  // 32*kh .. +31, so both halves of the merge and of the stores run at once.
+  float *slot = reinterpret_cast<float *>(lds_raw) + (size_t)wave * kMergeRegs * 64;
+  const float *other = reinterpret_cast<const float *>(lds_raw) + (size_t)(wave ^ 4) * kMergeRegs * 64;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      mbuf[r * 64 + lane] = o[0][r];
-      mbuf[(16 + r) * 64 + lane] = o[1][r];
-    }
-    mbuf[32 * 64 + lane] = m;
-    mbuf[33 * 64 + lane] = l;
-  }
+  for (int r = 0; r < 16; ++r) slot[r * 64 + lane] = kh == 0 ? o[1][r] : o[0][r];
+  slot[16 * 64 + lane] = m;
+  slot[17 * 64 + lane] = l;
   __syncthreads();
-  if (kh == 1 || !wave_active) return;
-  {
-    const float m1 = mbuf[32 * 64 + lane], l1 = mbuf[33 * 64 + lane];
-    const float mt = fmaxf(m, m1);
-    const float mu = (mt == -INFINITY) ? 0.f : mt;
-    const float a0 = fast_exp2(m - mu), a1 = fast_exp2(m1 - mu);
-    l = l * a0 + l1 * a1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o[0][r] = o[0][r] * a0 + mbuf[r * 64 + lane] * a1;
-      o[1][r] = o[1][r] * a0 + mbuf[(16 + r) * 64 + lane] * a1;
-    }
-    m = mt;
-  }
-  const float lt = pair_sum(l);
+  if (!wave_active) return;
+  const float mp = other[16 * 64 + lane], lp = other[17 * 64 + lane];
+  const float m0 = kh == 0 ? m : mp, m1 = kh == 0 ? mp : m;
+  const float l0 = kh == 0 ? l : lp, l1 = kh == 0 ? lp : l;
+  const float mt = fmaxf(m0, m1);
+  const float mu = (mt == -INFINITY) ? 0.f : mt;
+  const float a0 = fast_exp2(m0 - mu), a1 = fast_exp2(m1 - mu);
+  const float lt = pair_sum(l0 * a0 + l1 * a1);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (query < S) {
-    float *orow = O + (size_t)query * ld + hoff;
+    float *orow = O + (size_t)query * ld + hoff + kh * 32;
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int g = 0; g < 4; ++g) {
+      float v[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 val = make_float4(o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
-                                       o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-        *reinterpret_cast<float4 *>(orow + db * 32 + g * 8 + hh * 4) = val;
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * g + j;
+        const float mine = kh == 0 ? o[0][r] : o[1][r], theirs = other[r * 64 + lane];
+        const float x0 = kh == 0 ? mine : theirs, x1 = kh == 0 ? theirs : mine;
+        v[j] = (x0 * a0 + x1 * a1) * inv;
       }
-    if (LSE != nullptr && hh == 0)
-      LSE[(size_t)head * S + query] = lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+      *reinterpret_cast<float4 *>(orow + g * 8 + hh * 4) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (LSE != nullptr && kh == 0 && hh == 0)
+      LSE[(size_t)head * S + query] = lt > 0.f ? (mt + log2f(lt)) * kLn2 : -INFINITY;
   }
 }
 
