@@ -259,6 +259,12 @@ __device__ __forceinline__ void exchange_pair(float *buf, int wave, int lane, f3
     }
 }
 
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
 // dK and dV of keys [kv_blk0, kv_blk0 + 128) of one head. Wave w owns keys
 // kv_blk0 + 32*(w%4) .. +31 and query half w/4 of every 64-row block.
 //
@@ -334,45 +340,36 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 
   f32x16 dk[2], dv[2];
   dk[0] = dk[1] = dv[0] = dv[1] = f32x16{};
-  // The accumulators hold sigma_cur * (dK, dV), sigma_cur the dO scale of the
-  // blocks added so far; a block with another scale first moves them to its
-  // units (an exact power-of-two product). Every wave sees every block's scale
-  // in the same order, so partners end in the same units.
-  int sig_cur = __float_as_int(1.f);
-  // When every block the workgroup walks has one scale (the usual case:
-  // blocks of similar magnitude share it), the accumulators start in that
-  // unit and no block's scale is read back. (Zero accumulators in another
-  // unit equal zero in this one, so the results are those of the per-block
-  // checks.)
+  // dO scales. The accumulators hold sig_min * (dK, dV), sig_min the
+  // smallest dO scale of the blocks this item walks (that of the block of
+  // largest magnitude). A block with a larger scale sig_b adds its products
+  // scaled by sig_min / sig_b = 2^lr (lr a negative integer), which the
+  // scores' starting values carry into P's exponent (dS = P (dP - Delta)
+  // inherits the factor), so the accumulators never move to a larger unit and
+  // cannot overflow for finite inputs; contributions that the factor pushes
+  // below the fp16 range are negligible against the block of largest
+  // magnitude. When every block has one scale (the usual case: blocks of
+  // similar magnitude share it) no block's scale is read back.
+  int sig_min;
   bool sig_uniform;
   {
     const float *sg = a.sigma + (size_t)head * a.n_blocks;
-    const int s0 = __builtin_amdgcn_readfirstlane(__float_as_int(sg[min(first_qb, a.n_blocks - 1)]));
+    const float s0 = sg[min(first_qb, a.n_blocks - 1)];
+    float mn = s0;
     bool differs = false;
-    for (int b = first_qb + lane; b < n_qblocks; b += 64) differs |= __float_as_int(sg[b]) != s0;
+    for (int b = first_qb + lane; b < n_qblocks; b += 64) {
+      const float sb = sg[b];
+      differs |= sb != s0;
+      mn = fminf(mn, sb);
+    }
     sig_uniform = !__any(differs);
-    if (sig_uniform) sig_cur = s0;
+    sig_min = __builtin_amdgcn_readfirstlane(__float_as_int(sig_uniform ? s0 : wave_min(mn)));
   }
 
   // One block. `masked`: the block may hold the causal diagonal, so rows
   // below this wave's keys are masked and a wave whose rows are all below
   // its keys skips the block.
   auto compute = [&](int i, int st, bool masked) {
-    if (!sig_uniform) {
-      const int sig_b = __builtin_amdgcn_readfirstlane(
-          __float_as_int(*reinterpret_cast<const float *>(stage_base(st) + kStageSigma)));
-      if (sig_b != sig_cur) {
-        const float ratio = __int_as_float(sig_b) / __int_as_float(sig_cur);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          dk[0][r] *= ratio;
-          dk[1][r] *= ratio;
-          dv[0][r] *= ratio;
-          dv[1][r] *= ratio;
-        }
-        sig_cur = sig_b;
-      }
-    }
     const int q0 = (first_qb + i) * kQBlock + qh * 32;  // this wave's first query row
     if (masked && q0 + 31 < key0) return;
     const half_t *qt = reinterpret_cast<const half_t *>(stage_base(st));
@@ -387,6 +384,15 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
       const float4 nd = *reinterpret_cast<const float4 *>(sl + kQBlock + qh * 32 + g * 8 + hh * 4);
       s[4 * g] = nl.x; s[4 * g + 1] = nl.y; s[4 * g + 2] = nl.z; s[4 * g + 3] = nl.w;
       dp[4 * g] = nd.x; dp[4 * g + 1] = nd.y; dp[4 * g + 2] = nd.z; dp[4 * g + 3] = nd.w;
+    }
+    if (!sig_uniform) {
+      const int sig_b = __builtin_amdgcn_readfirstlane(
+          __float_as_int(*reinterpret_cast<const float *>(stage_base(st) + kStageSigma)));
+      if (sig_b != sig_min) {
+        const float lr = (float)(((sig_min >> 23) & 0xff) - ((sig_b >> 23) & 0xff));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] += lr;
+      }
     }
     half8_t qa[4], ga[4];
 #pragma unroll
@@ -502,7 +508,7 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
 #pragma unroll
     for (int r = 0; r < 16; ++r) res[db][r] = qh == 0 ? dk[db][r] : dv[db][r];
   float *out = qh == 0 ? a.dK : a.dV;
-  const float sigma = __int_as_float(sig_cur);
+  const float sigma = __int_as_float(sig_min);
   const float out_scale = qh == 0 ? kLn2 / sigma : 1.f / sigma;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {

@@ -189,7 +189,8 @@ void darkforest_sync(void);
  * rounded to fp16, so their magnitudes must stay below 65504 (fp16's largest
  * finite value); beyond it they overflow and the outputs are not finite.
  * d_out needs no such bound (each 64-row block is scaled by a power of two
- * before rounding). Other d_head values run in fp32 like the reference.   */
+ * before rounding, and dK, dV are summed in the units of the block of
+ * largest magnitude). Other d_head values run in fp32 like the reference. */
 
 /* Forward: O [S, H*D] and lse [H, S] (lse may be NULL to skip it).
  * No allocation: only the caller's Q, K, V, O and lse are touched.

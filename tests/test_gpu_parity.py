@@ -143,12 +143,13 @@ def test_ragged_seq_len(device, seq_len, causal):
             oracle_fwd_bwd(x, 3, 0.125, causal), scaled=True)
 
 
-@pytest.mark.parametrize("seq_len,n_heads", [(2049, 5), (3071, 2), (4097, 3)])
+@pytest.mark.parametrize("seq_len,n_heads", [(2049, 5), (3071, 2), (4097, 3), (4097, 5), (2049, 12)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_long_ragged_seq_len(device, seq_len, n_heads, causal):
     """Lengths just past and short of the 64-key and 128-row tiles at the scale of C2, odd head
     counts: the masked tails, the pipelined loops' remainders and the backward's last pair, through
-    both the one-call path and the timed training sequence."""
+    both the one-call path and the timed training sequence. The last two shapes launch more
+    backward workgroups than the device has compute units (a second dispatch round)."""
     say(f"long ragged S={seq_len} H={n_heads} causal={causal}")
     x = O.seeded_inputs(seq_len, n_heads, 64, 8000 + seq_len + n_heads)
     want = oracle_fwd_bwd(x, n_heads, 0.125, causal)
@@ -217,9 +218,10 @@ def test_forward_reference_point_moves(device, causal):
 @pytest.mark.parametrize("causal", [True, False])
 def test_dO_blocks_of_different_magnitudes(device, causal):
     """Each 64-row block of dO gets its own power-of-two scale in the backward. Blocks scaled by 1/16,
-    1 and 16 in turn get three different scales, so the dK/dV accumulators change units between
-    blocks (a wrong unit would be off by 16x or more). Both the one-call backward and the timed
-    training sequence are compared with the oracle."""
+    1 and 16 in turn get three different scales: the dK/dV accumulators hold the units of the
+    smallest and the other blocks' products are scaled into them (a wrong factor would be off by
+    16x or more). Both the one-call backward and the timed training sequence are compared with the
+    oracle."""
     say(f"dO blocks scaled 1/16, 1, 16 in turn, H=2 S=1000 causal={causal}")
     x = O.seeded_inputs(1000, 2, 64, 7100 + int(causal))
     mags = np.array([1 / 16, 1.0, 16.0], np.float32)
@@ -227,6 +229,24 @@ def test_dO_blocks_of_different_magnitudes(device, causal):
     want = oracle_fwd_bwd(x, 2, 0.125, causal)
     compare(f"one call c={int(causal)}", run_fwd_bwd(x, 2, 0.125, causal, device), want, scaled=True)
     compare(f"training pair c={int(causal)}", run_training_pair(x, 2, 0.125, causal, device), want, scaled=True)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_dO_block_near_fp32_underflow(device, causal):
+    """A 64-row dO block of magnitude ~1e-37 between N(0,1) blocks: its scale is 2^125 against the
+    others' 2, and the dK/dV accumulators keep the units of the largest-magnitude block (the
+    smallest scale), so the tiny block's products are scaled down before their fp16 rounding instead
+    of the accumulators being scaled up by 2^124 (which overflows). Two shapes: H=2, S=1000 and
+    C2's H=12, S=4096."""
+    for n_heads, seq_len in ((2, 1000), (12, 4096)):
+        say(f"dO block 5 of magnitude 1e-37, H={n_heads} S={seq_len} causal={causal}")
+        x = O.seeded_inputs(seq_len, n_heads, 64, 7300 + int(causal) + seq_len)
+        x["do"][5 * 64:6 * 64] *= np.float32(1e-37)
+        want = oracle_fwd_bwd(x, n_heads, 0.125, causal)
+        compare(f"tiny block H={n_heads} c={int(causal)}", run_fwd_bwd(x, n_heads, 0.125, causal, device), want,
+                scaled=True)
+        compare(f"tiny block pair H={n_heads} c={int(causal)}", run_training_pair(x, n_heads, 0.125, causal, device),
+                want, scaled=True)
 
 
 # ---------------------------------------------------------------- known-answer tests of the reference
