@@ -40,6 +40,17 @@ namespace {
 
 constexpr int kPreRows = 64;  // rows per phase-1 workgroup (one dO scale per block)
 inline int pre_blocks(int S) { return (S + kPreRows - 1) / kPreRows; }
+// Under causal masking the first keys of a head see few query rows, with
+// probabilities near one (row 0 sees key 0 alone), so one fp16 rounding of
+// dO, dS or Q in rows 0-63 lands almost undamped in dV and dK of those keys:
+// for N(0,1) inputs these are the largest absolute errors of the backward.
+// The dK/dV workgroup of keys 0-127 therefore adds the rounding residues of
+// those rows (lo = fp16(x - fp16(x)) of sigma*dO, c2*Q and dS) with three
+// more products per block: dV += P^T dO_lo, dK += dS_lo^T (c2 Q) + dS^T (c2 Q)_lo.
+// Likewise the dQ workgroup of rows 0-127 adds, for keys 0-63 (its first
+// tile), dQ += dS K_lo + dS_lo K.
+constexpr int kLoRows = 64;
+constexpr int kLoTiles = 3;  // per head: sigma*dO, c2*Q, K (rows 0-63)
 
 // Power-of-two scale of a 64-row block of dO: sigma = 2^e with e = 1 (mod 4)
 // and max|sigma * x| in [2, 32) for amax = max|x| (1 if amax is 0 or not
@@ -84,9 +95,13 @@ constexpr int kOwnTile = 128 * kD;  // halves
 constexpr int kOwnBytes = 2 * kOwnTile * 2;
 // Last, the dQ workgroup's 128 values of -lse*log2(e) and of -Delta*sigma.
 constexpr int kRowStatBytes = 2 * 128 * 4;
-constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes + kRowStatBytes;
-constexpr int kOwnOffset = kLdsBytes - kRowStatBytes - kOwnBytes;
-constexpr int kRowStatOffset = kLdsBytes - kRowStatBytes;
+// Then the dK/dV workgroup of keys 0-127 (causal) keeps the residue tiles of
+// rows 0-63, sigma*dO_lo and (c2 Q)_lo, as two [64][64] fp16 tiles.
+constexpr int kLoBytes = 2 * kTile * 2;
+constexpr int kLdsBytes = (kRingBytes > kMergeBytes ? kRingBytes : kMergeBytes) + kOwnBytes + kRowStatBytes + kLoBytes;
+constexpr int kOwnOffset = kLdsBytes - kLoBytes - kRowStatBytes - kOwnBytes;
+constexpr int kRowStatOffset = kLdsBytes - kLoBytes - kRowStatBytes;
+constexpr int kLoOffset = kLdsBytes - kLoBytes;
 
 template <int N>
 using Const = std::integral_constant<int, N>;
@@ -94,9 +109,11 @@ using Const = std::integral_constant<int, N>;
 // Workspace layout (bytes, each part 256-byte aligned): the dO scale of
 // every 64-row block, sigma [H][ceil(S/64)] fp32; the row statistics as the
 // main kernel's products take them, -lse*log2(e) and -Delta*sigma_b, each
-// [H][S] fp32; the fp16 copies c2*Q, K, V and sigma_b*dO, each [H][S][64].
+// [H][S] fp32; the fp16 copies c2*Q, K, V and sigma_b*dO, each [H][S][64];
+// the fp16 rounding residues of rows 0-63 of sigma_b*dO, c2*Q and K,
+// [H][3][64][64] (see kLoRows).
 struct WsLayout {
-  size_t sigma, lse2n, deltan, q16, k16, v16, do16, total;
+  size_t sigma, lse2n, deltan, q16, k16, v16, do16, lo16, total;
 };
 inline size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 inline WsLayout ws_layout(int H, int S) {
@@ -110,7 +127,8 @@ inline WsLayout ws_layout(int H, int S) {
   w.k16 = w.q16 + copy;
   w.v16 = w.k16 + copy;
   w.do16 = w.v16 + copy;
-  w.total = w.do16 + copy;
+  w.lo16 = w.do16 + copy;
+  w.total = w.lo16 + align256((size_t)H * kLoTiles * kLoRows * kD * sizeof(half_t));
   return w;
 }
 
@@ -128,7 +146,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const float *__restrict__ O, const float *__restrict__ dO, const float *__restrict__ lse,
     float *__restrict__ sigma_out, float *__restrict__ lse2n, float *__restrict__ deltan,
     half_t *__restrict__ q16, half_t *__restrict__ k16, half_t *__restrict__ v16, half_t *__restrict__ do16,
-    int H, int S, float c2, int convert_qkv, int ldi) {
+    half_t *__restrict__ lo16, int H, int S, float c2, int convert_qkv, int ldi) {
   __shared__ float wmax[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int head = blockIdx.y;
@@ -152,6 +170,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[t][i] = load4_or_zero(in[t] + src_in + 16 * i, ok);
   }
+  const bool lo_block = blockIdx.x == 0;
   const float l = ok ? lse[r] : 0.f;
   float mx = 0.f;
 #pragma unroll
@@ -182,7 +201,27 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) *reinterpret_cast<half4_t *>(do16 + dst + 16 * i) = h[i];
+  // Rows 0-63: the rounding residues fp16(x - fp16(x)) of sigma_b*dO and (when
+  // this launch converts Q, K and V; otherwise the training forward wrote
+  // them) of c2*Q and K, x the fp32 value the fp16 copy was rounded from (the
+  // difference is exact in fp32).
+  half_t *lo = lo16 + ((size_t)head * kLoTiles * kLoRows + row) * kD + (tid & 3) * 4;
+  if (lo_block) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 gp = scale4(g[i], sig);
+      *reinterpret_cast<half4_t *>(lo + 16 * i) = to_half4(make_float4(
+          gp.x - (float)h[i][0], gp.y - (float)h[i][1], gp.z - (float)h[i][2], gp.w - (float)h[i][3]));
+    }
+  }
   if (!convert_qkv) return;
+  if (lo_block) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<half4_t *>(lo + kLoRows * kD + 16 * i) = scaled_residue4(x[0][i], c2);
+      *reinterpret_cast<half4_t *>(lo + 2 * kLoRows * kD + 16 * i) = scaled_residue4(x[1][i], 1.f);
+    }
+  }
   half_t *out[3] = {q16, k16, v16};
 #pragma unroll
   for (int t = 0; t < 3; ++t)
@@ -202,7 +241,7 @@ constexpr int kCostQStep = 25;
 // (c2 = scale*log2(e), the forward's rounding), K, V and sigma_b*dO (sigma_b
 // the power-of-two scale of the row's 64-row block, sigma [H][n_blocks]).
 struct BwdArgs {
-  const half_t *Q16, *K16, *V16, *dO16;
+  const half_t *Q16, *K16, *V16, *dO16, *lo16;
   const float *lse2n, *deltan, *sigma;
   float *dQ, *dK, *dV;
   int H, S, causal, n_blocks;
@@ -294,6 +333,8 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   // Under causal masking the first two blocks hold the diagonal of the
   // workgroup's 128 keys; every later row sees every key.
   const int i0 = a.causal ? 2 : 0;
+  // The workgroup of keys 0-127 adds the first block's rounding residues (kLoRows).
+  const bool lo_corr = a.causal && kv_blk0 == 0;
 
   // Per-thread offsets, fixed for the whole loop: rows qh*32 + c of a tile
   // (A operands of S and dP), this wave's transposed reads (B operands of dV
@@ -441,6 +482,29 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
         dk[db] = mfma32x32x16(dsf, qtr[j][db], dk[db]);
       }
     }
+    // Rows 0-63 (the first block of keys 0-127): the residues' products,
+    // dV += P^T dO_lo, dK += dS^T (c2 Q)_lo + dS_lo^T (c2 Q).
+    if (masked && lo_corr && i == 0) {
+      const half_t *glo = reinterpret_cast<const half_t *>(lds_raw + kLoOffset);
+      const half_t *qlo = glo + kTile;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8_t pf = acc_to_slots(s, j);
+        const half8_t dsf = acc_to_slots(dp, j);
+        half8_t dsl;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) dsl[jj] = (half_t)(dp[8 * j + jj] - (float)dsf[jj]);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const half4_t g0 = tile_tr4_at(glo, troff[j][db][0]), g1 = tile_tr4_at(glo, troff[j][db][1]);
+          const half4_t q0v = tile_tr4_at(qlo, troff[j][db][0]), q1v = tile_tr4_at(qlo, troff[j][db][1]);
+          dv[db] = mfma32x32x16(pf, half8_t{g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]}, dv[db]);
+          dk[db] = mfma32x32x16(dsf, half8_t{q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]},
+                                dk[db]);
+          dk[db] = mfma32x32x16(dsl, qtr[j][db], dk[db]);
+        }
+      }
+    }
   };
 
   // Blocks go through the ring in pairs: iteration k computes blocks i = 2k
@@ -462,6 +526,15 @@ __device__ void dkdv_path(const BwdArgs &a, int head, int kv_blk0, unsigned char
   dma_rows128(a.V16, head, S, kv_blk0, lds_raw + kOwnOffset + kOwnTile * 2);
   dma_block(0, (0 - i0) & 3);
   dma_block(1, (1 - i0) & 3);
+  // The residue tiles of rows 0-63 (the first block) for the workgroup of
+  // keys 0-127 (rows past S read as zeros).
+  if (lo_corr) {
+    const unsigned nrec = (unsigned)min(S, kLoRows) * kD * 2;
+    const half_t *lo = a.lo16 + (size_t)head * kLoTiles * kLoRows * kD;
+    const unsigned lt = lds_addr32(lds_raw + kLoOffset + wave * 1024);
+    lds_fetch16(sgpr_rsrc(lo, nrec), lt, dma_off);
+    lds_fetch16(sgpr_rsrc(lo + kLoRows * kD, nrec), lt + kTile * 2, dma_off);
+  }
   lds_fetch_barrier<0>();
   {
     // K^T / V^T fragments (B operands of S = Q K^T and dP = dO V^T): lane c
@@ -538,6 +611,8 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // starting at k0 is masked for any row of the wave when k0 + 31 <= key_lim_lo.
   const int key_lim = a.causal ? min(query, S - 1) : S - 1;
   const int key_lim_lo = a.causal ? min(q_w0, S - 1) : S - 1;
+  // The workgroup of rows 0-127 adds the residues of keys 0-63 (kLoRows).
+  const bool lo_corr = a.causal && q_blk0 == 0;
 
   half8_t qf[4], gf[4];
   f32x16 negL, negD;
@@ -631,6 +706,23 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 #pragma unroll
       for (int db = 0; db < 2; ++db) dq[db] = mfma32x32x16(ktr[j][db], dsf, dq[db]);
     }
+    // Keys 0-63 (tile 0) of rows 0-127: dQ^T += K_lo^T dS^T + K^T dS_lo^T.
+    if (masked && lo_corr && t == 0) {
+      const half_t *klo = reinterpret_cast<const half_t *>(lds_raw + kLoOffset);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8_t dsf = acc_to_slots(dp, j);
+        half8_t dsl;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) dsl[jj] = (half_t)(dp[8 * j + jj] - (float)dsf[jj]);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const half4_t lo = tile_tr4_at(klo, ktoff[j][db][0]), hi = tile_tr4_at(klo, ktoff[j][db][1]);
+          dq[db] = mfma32x32x16(half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, dsf, dq[db]);
+          dq[db] = mfma32x32x16(ktr[j][db], dsl, dq[db]);
+        }
+      }
+    }
   };
   // One tile, unpipelined. `masked`: the tile may hold the causal diagonal or
   // the end of the keys; a wave that sees none of it skips it.
@@ -648,6 +740,13 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
   // first products wait for all but tiles 1 and 2.
   dma_rows128(a.Q16, head, S, q_blk0, lds_raw + kOwnOffset);
   dma_rows128(a.dO16, head, S, q_blk0, lds_raw + kOwnOffset + kOwnTile * 2);
+  // The residue tile of K's rows 0-63 for the workgroup of rows 0-127 (keys
+  // past S read as zeros).
+  if (lo_corr) {
+    const unsigned nrec = (unsigned)min(S, kLoRows) * kD * 2;
+    lds_fetch16(sgpr_rsrc(a.lo16 + ((size_t)head * kLoTiles + 2) * kLoRows * kD, nrec),
+                lds_addr32(lds_raw + kLoOffset + wave * 1024), dma_off);
+  }
   {
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     if (wave_u < 4) {
@@ -817,12 +916,15 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
 
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len) { return ws_layout(n_heads, seq_len).total; }
 
-void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16) {
+void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16,
+                       half_t **qlo, int *qlo_head_stride) {
   const WsLayout w = ws_layout(n_heads, seq_len);
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   *q16 = reinterpret_cast<half_t *>(ws + w.q16);
   *k16 = reinterpret_cast<half_t *>(ws + w.k16);
   *v16 = reinterpret_cast<half_t *>(ws + w.v16);
+  *qlo = reinterpret_cast<half_t *>(ws + w.lo16) + kLoRows * kD;
+  *qlo_head_stride = kLoTiles * kLoRows * kD;
 }
 
 hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, const float *o,
@@ -834,7 +936,8 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      lse, reinterpret_cast<float *>(ws + w.sigma), reinterpret_cast<float *>(ws + w.lse2n),
                      reinterpret_cast<float *>(ws + w.deltan), reinterpret_cast<half_t *>(ws + w.q16),
                      reinterpret_cast<half_t *>(ws + w.k16), reinterpret_cast<half_t *>(ws + w.v16),
-                     reinterpret_cast<half_t *>(ws + w.do16), n_heads, seq_len, scale * kLog2e,
+                     reinterpret_cast<half_t *>(ws + w.do16), reinterpret_cast<half_t *>(ws + w.lo16), n_heads,
+                     seq_len, scale * kLog2e,
                      qkv_saved ? 0 : 1, ldi > 0 ? ldi : n_heads * kD);
   return hipGetLastError();
 }
@@ -849,6 +952,7 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
   a.K16 = reinterpret_cast<const half_t *>(ws + w.k16);
   a.V16 = reinterpret_cast<const half_t *>(ws + w.v16);
   a.dO16 = reinterpret_cast<const half_t *>(ws + w.do16);
+  a.lo16 = reinterpret_cast<const half_t *>(ws + w.lo16);
   a.lse2n = reinterpret_cast<const float *>(ws + w.lse2n);
   a.deltan = reinterpret_cast<const float *>(ws + w.deltan);
   a.sigma = reinterpret_cast<const float *>(ws + w.sigma);

@@ -58,6 +58,9 @@ constexpr int kMergeBytes = kWaves * kMergeRegs * 64 * 4;
 constexpr int kQTileBytes = kBM * kD * 2;
 constexpr int kQF4 = kBM * kD / 4 / kThreads;  // float4 of Q per thread
 constexpr int kLdsBytes = (kMergeBytes > kRingBytes ? kMergeBytes : kRingBytes) + kQTileBytes;
+// Rows of each head whose c2*Q and K rounding residues the training forward
+// writes for the backward (its correction of the first keys and rows).
+constexpr int kLoRows = 64;
 
 template <int N>
 using Stage = std::integral_constant<int, N>;
@@ -75,11 +78,14 @@ __device__ __forceinline__ half4_t lds_tr4(const unsigned char *p) {
 // registers. Under causal masking the K and V rows of its own query tile are
 // the last key tiles the workgroup stages, and it writes them from LDS after
 // the loop; without masking each workgroup copies those rows from the
-// inputs at the end.
+// inputs at the end. QLO (with Q16): the residues fp16(x - fp16(x)) of each
+// head's rows 0-63 of c2*Q and then of K, two [64][64] tiles every
+// qlo_stride halves, which the backward adds for the first keys and rows.
 __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
     const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ V,
     float *__restrict__ O, float *__restrict__ LSE, int H, int S, float qscale, int causal,
-    int n_qtiles, half_t *__restrict__ Q16, half_t *__restrict__ K16, half_t *__restrict__ V16, int ldi) {
+    int n_qtiles, half_t *__restrict__ Q16, half_t *__restrict__ K16, half_t *__restrict__ V16,
+    half_t *__restrict__ QLO, int qlo_stride, int ldi) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -305,9 +311,19 @@ __global__ __launch_bounds__(kThreads) void fwd_d64_kernel(
       *reinterpret_cast<half4_t *>(qt + tile_off(idx >> 4, (idx & 15) * 4)) = qh;
       const int row = q_blk0 + (idx >> 4);
       if (save && row < S) *reinterpret_cast<half4_t *>(Q16 + ((size_t)head * S + row) * kD + (idx & 15) * 4) = qh;
+      if (save && row < min(S, kLoRows))
+        *reinterpret_cast<half4_t *>(QLO + (size_t)head * qlo_stride + row * kD + (idx & 15) * 4) =
+            scaled_residue4(qraw[k], qscale);
     }
 #pragma unroll
     for (int p = 0; p < 3; ++p) store_rows(kstage(p), kp[p]);
+    // The workgroup of query tile 0 also writes the residues of K's rows 0-63
+    // (key tile 0), one granule of 8 values per thread.
+    if (save && qtile == 0 && (tid >> 3) < min(S, kLoRows)) {
+      half_t *dst = QLO + (size_t)head * qlo_stride + kLoRows * kD + (tid >> 3) * kD + (tid & 7) * 8;
+      const half4_t lo = scaled_residue4(kp[0][0], 1.f), hi = scaled_residue4(kp[0][1], 1.f);
+      *reinterpret_cast<half8_t *>(dst) = half8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
     store_rows(vstage(0), vp);
     *reinterpret_cast<half8_t *>(vstage(-1) + tid * 16) = half8_t{};
   }
@@ -595,10 +611,12 @@ hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float 
                           hipStream_t stream, void *bwd_workspace, int ldi) {
   const int n_qtiles = (seq_len + kBM - 1) / kBM;
   const dim3 grid((unsigned)(n_qtiles * n_heads));
-  half_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr;
-  if (bwd_workspace != nullptr) bwd_ws_qkv_copies(bwd_workspace, n_heads, seq_len, &q16, &k16, &v16);
+  half_t *q16 = nullptr, *k16 = nullptr, *v16 = nullptr, *qlo = nullptr;
+  int qlo_stride = 0;
+  if (bwd_workspace != nullptr)
+    bwd_ws_qkv_copies(bwd_workspace, n_heads, seq_len, &q16, &k16, &v16, &qlo, &qlo_stride);
   hipLaunchKernelGGL(fwd_d64_kernel, grid, dim3(kThreads), 0, stream, q, k, v, o, lse, n_heads,
-                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles, q16, k16, v16,
+                     seq_len, scale * kLog2e, causal ? 1 : 0, n_qtiles, q16, k16, v16, qlo, qlo_stride,
                      ldi > 0 ? ldi : n_heads * kD);
   return hipGetLastError();
 }

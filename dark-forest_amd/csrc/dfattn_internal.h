@@ -130,6 +130,15 @@ __device__ __forceinline__ half4_t round_scaled4(float4 v, float s) {
   return to_half4(p);
 }
 
+// fp16(p - fp16(p)) for p = fp32(v * s): what round_scaled4 rounds away
+// (the difference is exact in fp32).
+__device__ __forceinline__ half4_t scaled_residue4(float4 v, float s) {
+  float4 p = scale4(v, s);
+  asm volatile("" : "+v"(p.x), "+v"(p.y), "+v"(p.z), "+v"(p.w));
+  const half4_t h = to_half4(p);
+  return to_half4(make_float4(p.x - (float)h[0], p.y - (float)h[1], p.z - (float)h[2], p.w - (float)h[3]));
+}
+
 __device__ __forceinline__ float4 load4_or_zero(const float *p, bool ok) {
   return ok ? *reinterpret_cast<const float4 *>(p) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
@@ -265,8 +274,11 @@ hipError_t launch_fwd_d64(const float *q, const float *k, const float *v, float 
 
 // Backward, D = 64, MFMA. Needs bwd_workspace_bytes_d64() of workspace.
 size_t bwd_workspace_bytes_d64(int n_heads, int seq_len);
-// Where the fp16 copies of c2*Q, K and V sit in a backward workspace.
-void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16);
+// Where the fp16 copies of c2*Q, K and V sit in a backward workspace, and
+// the residues fp16(x - fp16(x)) of each head's rows 0-63 of c2*Q and K (two
+// [64][64] fp16 tiles per head from *qlo, `qlo_head_stride` halves apart).
+void bwd_ws_qkv_copies(void *workspace, int n_heads, int seq_len, half_t **q16, half_t **k16, half_t **v16,
+                       half_t **qlo, int *qlo_head_stride);
 hipError_t launch_bwd_d64(const float *q, const float *k, const float *v, const float *o,
                           const float *d_o, const float *lse, float *d_q, float *d_k,
                           float *d_v, void *workspace, int n_heads, int seq_len, float scale,

@@ -88,11 +88,12 @@ def test_backward_validation():
 
 def test_backward_workspace_is_linear_in_seq_len():
     lib = dfattn.lib()
-    # The per-64-row-block dO scales [H, ceil(S/64)], two fp32 row statistics [H, S] and four
-    # fp16 copies [H, S, 64] (c2*Q, K, V, sigma*dO), each rounded up to 256 bytes.
+    # The per-64-row-block dO scales [H, ceil(S/64)], two fp32 row statistics [H, S], four fp16
+    # copies [H, S, 64] (c2*Q, K, V, sigma*dO) and the fp16 rounding residues of rows 0-63 of
+    # sigma*dO, c2*Q and K [H, 3, 64, 64], each rounded up to 256 bytes.
     up = lambda x: (x + 255) // 256 * 256
     for h, s in ((12, 1024), (12, 4096), (1, 5), (12, 131072)):
-        want = up(h * ((s + 63) // 64) * 4) + 2 * up(h * s * 4) + 4 * up(h * s * 64 * 2)
+        want = up(h * ((s + 63) // 64) * 4) + 2 * up(h * s * 4) + 4 * up(h * s * 64 * 2) + up(h * 3 * 64 * 64 * 2)
         assert lib.dfattn_bwd_workspace_bytes(h, s, 64) == want
     assert lib.dfattn_bwd_workspace_bytes(0, 10, 64) == 0
     # O(H*S*D), against the reference's O(H*S^2) probability scratch (lib.rs:2023): 1/64 of it at S = 4096.

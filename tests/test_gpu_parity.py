@@ -122,11 +122,14 @@ def run_training_pair(x, n_heads, scale, causal, device):
     return {"o": host(o), "lse": host(lse), "dq": host(grads[0]), "dk": host(grads[1]), "dv": host(grads[2])}
 
 
-@pytest.mark.parametrize("seq_len,seed", [(1024, 2000), (1024, 2500), (4096, 3000), (4096, 3500)])
+@pytest.mark.parametrize("seq_len,seed", [(1024, 2000), (1024, 2500), (1024, 2050), (1024, 2100), (4096, 3000),
+                                          (4096, 3500), (4096, 3600), (4096, 3800), (4096, 4100)])
 def test_timed_training_pair_matches_oracle(device, seq_len, seed):
     """The sequence bench.py times (C1 and C2 shapes; seed 3000 is bench.py's own input) against the
-    oracle at the north star's bar, on two seeds each. Prints every tensor's max-abs / rel-L2 so the
-    margin to the 2e-3 bar is on record."""
+    oracle at the north star's bar. Prints every tensor's max-abs / rel-L2 so the margin to the 2e-3
+    bar is on record. Of the 32 seeds of tests/golden/parity_margin_c1_c2.json, 2050 (C1) has the
+    largest dV error, 3600 and 3800 (C2) the largest dQ and dK errors; 2100 (C1, dV) and 4100 (C2,
+    dQ) exceed 2e-3 without the residue corrections of the first rows and keys."""
     say(f"timed training pair H=12 S={seq_len} seed {seed}")
     x = O.seeded_inputs(seq_len, 12, 64, seed)
     compare(f"pair S={seq_len} seed={seed}", run_training_pair(x, 12, 0.125, True, device),
