@@ -19,11 +19,13 @@ library launches on, around `steps` back-to-back launches of each phase in a
 second pass after the timed one; `frac_at_sclk` also divides by the peak at
 the shader clock rocm-smi reports while the step runs; `traffic` comes from
 the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary only when that summary
-was taken on this build's kernel sources, else null); `cpu_baseline` times
-the CPU oracle (a restatement of the reference's fp32 CPU attention) on a
-bounded sample of the same workload on one thread, `cpu_baseline_threads` on
+was taken on this build's kernel sources, else null); `gpu_configs` times every
+BASELINE attention config (C0-C3) on the GPU; `cpu_baseline` times the CPU
+oracle (a restatement of the reference's fp32 CPU attention) on the same
+workload on one thread (all 12 heads, about 16 s), `cpu_baseline_threads` on
 every head in parallel, `cpu_baseline_configs` every BASELINE attention
-config (C3 extrapolated from sampled rows).
+config (C3 extrapolated from 64 sampled rows). `gpt2_step_ms` is the eager
+GPT-2 small step, as the reference times it.
 """
 from __future__ import annotations
 
@@ -105,9 +107,9 @@ def cpu_baseline_configs(c2_one_thread=None):
     """The CPU oracle, 1 thread, on every BASELINE attention config (C0-C3), in ms and GFLOP/s.
 
     C0 (fwd, S=128) and C1 (fwd+bwd, S=1024) run in full, median of 3. C2 (fwd+bwd, S=4096) is the
-    `cpu_baseline` sample (6 of 12 heads) scaled to 12 heads. C3 (fwd, S=131072) is extrapolated:
-    the oracle's forward on a stratified sample of query rows (every head), timed, scaled by the
-    exact number of causal (query, key) pairs S(S+1)/2 over the sample's pairs.
+    `cpu_baseline` run (all 12 heads unless --cpu-heads says fewer, then scaled to 12). C3 (fwd,
+    S=131072) is extrapolated: the oracle's forward on 64 stratified query rows (every head), timed,
+    scaled by the exact number of causal (query, key) pairs S(S+1)/2 over the sample's pairs.
     """
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -139,12 +141,14 @@ def cpu_baseline_configs(c2_one_thread=None):
                  "how": "full, median of 3"})
     if c2_one_thread is not None:
         dt = c2_one_thread["seconds"] * H / c2_one_thread["heads"]
+        how = ("full, 1 run" if c2_one_thread["heads"] == H
+               else f"{c2_one_thread['heads']} of {H} heads timed, scaled to {H}")
         rows.append({"config": "C2 fwd+bwd S=4096", "ms": round(dt * 1e3, 1), "gflops": round(FLOP_STEP / dt / 1e9, 3),
-                     "how": f"{c2_one_thread['heads']} of {H} heads timed, scaled to {H}"})
+                     "how": how})
     s3 = 131072
     x = O.seeded_inputs(s3, H, D, 9000, std=0.5, with_grad=False)
-    sample = np.unique(np.concatenate([np.linspace(0, s3 - 1, 5).astype(np.int64),
-                                       np.random.default_rng(3).integers(0, s3, 3)]))
+    sample = np.unique(np.concatenate([np.linspace(0, s3 - 1, 32).astype(np.int64),
+                                       np.random.default_rng(3).integers(0, s3, 32)]))
     t0 = time.perf_counter()
     O.mha_forward_rows(x["q"], x["k"], x["v"], sample, H, SCALE, True, threads=1)
     dt = time.perf_counter() - t0
@@ -491,6 +495,107 @@ def seq_limit(max_alloc_s):
         torch.cuda.empty_cache()
 
 
+GPU_CONFIGS = (  # (name, S, fwd+bwd?, input std); H=12, D=64, causal, scale 1/8 (BASELINE configs[0..3])
+    ("C0 fwd S=128", 128, False, 1.0),
+    ("C1 fwd+bwd S=1024", 1024, True, 1.0),
+    ("C2 fwd+bwd S=4096", 4096, True, 1.0),
+    ("C3 fwd S=131072", 131072, False, 0.5),
+)
+
+
+def gpu_configs(warmup=10, timed=50, preheat=0.3):
+    """Every BASELINE attention config on the GPU: `preheat` seconds of back-to-back calls and
+    `warmup` untimed calls, then `timed` calls each between two HIP events on the library's stream; median, min and p90 ms, TFLOP/s at the median
+    (the reference's FLOP convention) and its fraction of the 2.5 PFLOP/s dense peak. C0 and C3 are
+    the plain forward (dfattn_fwd: O and lse), C1 and C2 the timed training step (dfattn_fwd_train,
+    dfattn_bwd_preprocess, dfattn_bwd_main). C3 also records the device memory the inputs and
+    outputs took and what the forward allocated beyond them (torch.cuda.mem_get_info before and
+    after), against the reference's rule that only Q, K, V, O (and lse) may be allocated."""
+    import ctypes
+
+    import torch
+
+    import dfattn
+
+    lib = dfattn.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sc = ctypes.c_float(SCALE)
+    rows = []
+    for name, s_len, train, std in GPU_CONFIGS:
+        torch.cuda.synchronize()
+        free0, _ = torch.cuda.mem_get_info()
+        gen = torch.Generator(device=dev).manual_seed(6000 + s_len)
+        q, k, v = (torch.randn(s_len, H * D, generator=gen, device=dev) * std for _ in range(3))
+        o = torch.empty_like(q)
+        lse = torch.empty((H, s_len), dtype=torch.float32, device=dev)
+        if train:
+            g = torch.randn(s_len, H * D, generator=gen, device=dev)
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+            ws = torch.empty(dfattn.bwd_workspace_bytes(H, s_len, D) // 4, dtype=torch.float32, device=dev)
+            wb = ws.numel() * 4
+            a_fwd = (ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), ptr(ws), wb, H, s_len, D, sc, 1, sp)
+            a_pre = (ptr(q), ptr(k), ptr(v), ptr(o), ptr(g), ptr(lse), ptr(ws), wb, H, s_len, D, sc,
+                     dfattn.BWD_QKV_SAVED, sp)
+            a_main = (ptr(q), ptr(k), ptr(v), ptr(o), ptr(g), ptr(lse), ptr(dq), ptr(dk), ptr(dv), ptr(ws), wb,
+                      H, s_len, D, sc, 1, sp)
+
+            def call():
+                if lib.dfattn_fwd_train(*a_fwd) | lib.dfattn_bwd_preprocess(*a_pre) | lib.dfattn_bwd_main(*a_main):
+                    raise RuntimeError(lib.dfattn_last_error_message().decode())
+            flop = 7.0 * H * s_len * s_len * D
+        else:
+            a_fwd = (ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), H, s_len, D, sc, 1, sp)
+
+            def call():
+                if lib.dfattn_fwd(*a_fwd):
+                    raise RuntimeError(lib.dfattn_last_error_message().decode())
+            flop = 2.0 * H * s_len * s_len * D
+        torch.cuda.synchronize()
+        free1, _ = torch.cuda.mem_get_info()
+        n_warm, n_timed = (3, 10) if s_len > 16384 else (warmup, timed)
+        # The clock falls back during the short configs and the host gaps between configs: run
+        # the call back to back for `preheat` seconds first, as the headline's timing does.
+        t_heat = time.perf_counter()
+        while time.perf_counter() - t_heat < preheat:
+            for _ in range(n_warm):
+                call()
+            torch.cuda.synchronize()
+        for _ in range(n_warm):
+            call()
+        torch.cuda.synchronize()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n_timed)]
+        for e0, e1 in ev:
+            e0.record(stream)
+            call()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        free2, _ = torch.cuda.mem_get_info()
+        ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+        med = ms[len(ms) // 2]
+        row = {"config": name, "H": H, "S": s_len, "D": D, "causal": True,
+               "calls": "dfattn_fwd_train + dfattn_bwd_preprocess + dfattn_bwd_main" if train else "dfattn_fwd",
+               "warmup": n_warm, "timed": n_timed, "median_ms": round(med, 5), "min_ms": round(ms[0], 5),
+               "p90_ms": round(ms[min(len(ms) - 1, (9 * len(ms)) // 10)], 5),
+               "gflop": round(flop / 1e9, 4), "tflops_at_median": round(flop / (med * 1e-3) / 1e12, 2),
+               "pct_mfma_peak": round(100 * flop / (med * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 2)}
+        if not train:
+            # (torch's allocator rounds each tensor up to its block size: for C0 the 1.5 MB of
+            # tensors take 6 MB of blocks)
+            row["alloc"] = {"inputs_outputs_mb": round((free0 - free1) / 2 ** 20, 2),
+                            "q_k_v_o_lse_mb": round((4 * s_len * H * D * 4 + H * s_len * 4) / 2 ** 20, 2),
+                            "during_forward_mb": round((free1 - free2) / 2 ** 20, 2)}
+        log(f"{name}: median {med:.4f} ms ({row['tflops_at_median']} TFLOP/s)")
+        rows.append(row)
+        del q, k, v, o, lse
+        if train:
+            del g, dq, dk, dv, ws
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -498,7 +603,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--preheat", type=float, default=0.3,
                     help="seconds of back-to-back steps before the warmup steps (clock ramp-up)")
-    ap.add_argument("--cpu-heads", type=int, default=6, help="heads in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU baseline sample (0 = skip)")
     ap.add_argument("--gpt2-steps", type=int, default=20,
                     help="timed GPT-2 small training steps at S=1024 (BASELINE configs[4]); 0 = skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -513,6 +618,8 @@ def main():
     ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
                     help="print the per-kernel mean of every counter of a rocprofv3 --pmc run and exit (no GPU)")
     ap.add_argument("--decode", type=int, default=1, help="1: also time KV-cache decode (result['decode'])")
+    ap.add_argument("--gpu-configs", type=int, default=1,
+                    help="1: also time every BASELINE attention config C0-C3 (result['gpu_configs'])")
     ap.add_argument("--flush-mib", type=int, default=1024,
                     help="cold-cache steps: MiB written before each of up to 20 event-timed steps (0 = skip)")
     ap.add_argument("--sclk", type=int, default=1,
@@ -709,6 +816,9 @@ def main():
                        "times steps that each follow a flush write). The device runs the step "
                        "back to back for `preheat.seconds` before the warmup steps, so the timed steps run at "
                        "the working clock rather than during the ramp from idle")
+    if args.gpu_configs:
+        log("every BASELINE attention config on the GPU (C0-C3)")
+        result["gpu_configs"] = gpu_configs()
     if args.decode:
         log("decode (KV cache, one query row per head)")
         result["decode"] = {"config": "H=12, D=64, one query; dfattn_decode with its workspace; bytes = K and V "
@@ -722,25 +832,28 @@ def main():
         eager = time_steps(model, steps=args.gpt2_steps, warmup=3)
         log(f"GPT-2 step median {eager['median_ms']:.2f} ms eager; now recorded into a HIP graph")
         g2 = time_steps(model, steps=args.gpt2_steps, warmup=3, graph=True)
-        result["gpt2_step_ms"] = round(g2["median_ms"], 3)
+        result["gpt2_step_ms"] = round(eager["median_ms"], 3)
         result["gpt2_step"] = {"config": "12 layers, d_model 768, 12 heads, d_ff 3072, vocab 50257, S=1024, batch 1",
                                "weights": "fp32, N(0,0.02) seeded", "tokens": "uniform [0,50257) seeded",
-                               "timing": "replays of one step recorded into a HIP graph (StaticGPT2.capture), "
-                                         "each followed by a device sync; eager_* = the same step dispatched "
-                                         "from Python each time",
+                               "timing": "gpt2_step_ms = eager_median_ms: the step dispatched from Python each "
+                                         "time and followed by a device sync, as the reference times its "
+                                         "step() calls (bench_darkforest_e2e.py:126-129); graph_replay_* = the "
+                                         "same step recorded once into a HIP graph (StaticGPT2.capture) and "
+                                         "replayed",
                                "engine": "explicit forward/backward on one activation allocation, attention "
                                          "through one dfattn context per layer, dfgpt2 kernels for embedding, "
                                          "LayerNorm, GELU, bias gradients, chunked fused cross-entropy and AdamW; "
                                          "hipBLASLt fp32 GEMMs",
-                               "median_ms": round(g2["median_ms"], 3), "min_ms": round(g2["min_ms"], 3),
                                "eager_median_ms": round(eager["median_ms"], 3),
                                "eager_min_ms": round(eager["min_ms"], 3),
+                               "graph_replay_median_ms": round(g2["median_ms"], 3),
+                               "graph_replay_min_ms": round(g2["min_ms"], 3),
                                "steps": args.gpt2_steps, "warmup": 3,
                                "loss_first": round(eager["losses"][0], 4), "loss_last": round(g2["losses"][-1], 4),
                                "peak_mem_mb": round(g2["peak_mem_mb"], 1),
                                "activation_arena_mb": round(model.activation_bytes() / 2 ** 20, 1)}
         del model
-        log(f"GPT-2 step median {g2['median_ms']:.2f} ms (graph replay)")
+        log(f"GPT-2 step median {g2['median_ms']:.2f} ms (graph replay); headline = eager {eager['median_ms']:.2f} ms")
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = torch.randn(n, device=dev)
