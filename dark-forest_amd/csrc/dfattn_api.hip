@@ -499,7 +499,12 @@ std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices] = {};
 
 // The scratch array's address on the current device (looked up on the first
-// call on each device, with that device current).
+// call on each device, with that device current). The first lookup makes the
+// runtime load this file's code object on the device and place the array: an
+// allocation inside the runtime, which a stream capture in global or
+// thread-local mode forbids. That first call may itself be under capture, so
+// the lookup runs with this thread's capture mode relaxed (and restored after);
+// it enqueues nothing on any stream, so nothing enters the captured graph.
 int scratch_on_current_device(const char *fn, void **out) {
   int dev = 0;
   hipError_t err = hipGetDevice(&dev);
@@ -509,7 +514,12 @@ int scratch_on_current_device(const char *fn, void **out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void *p = nullptr;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess) return record_hip(err, fn);
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t restore = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err == hipSuccess) err = restore;
     if (err != hipSuccess) return record_hip(err, fn);
     if (p == nullptr) return record_error(DFATTN_ERR_HIP, std::string(fn) + ": scratch symbol has no address");
     g_scratch_ptr[dev] = p;

@@ -249,50 +249,116 @@ __global__ __launch_bounds__(256) void embed_fwd_kernel(const uint32_t *__restri
   }
 }
 
-// grad_table[idx[p]] += sum of grad_out[q] over the positions q holding the
-// same id, in increasing q. Workgroup p scans the ids with wave ballots (64
-// per step): an equal id before p means another workgroup owns the row;
-// otherwise it adds grad_out[p] and every later match, in order, then adds
-// the sum to the table row. Each thread owns 4 columns (dim <= 4 * 256 per
-// pass, looping above that). Ids at or past rows_in_table are skipped.
+// grad_table[idx[p]] += the sum of grad_out[q] over the positions q holding
+// that id, in a fixed order. Workgroup p owns the id if no earlier position
+// holds it: its four waves scan the earlier ids, wave w the 64-position blocks
+// b = w (mod 4), and the workgroup leaves if any wave finds one. In the owner,
+// wave w sums the matching rows q >= p of its blocks in increasing q
+// (kRowsInFlight rows loaded ahead of the adds), and wave 0 adds
+// ((s0 + s1) + s2) + s3 to the table row: bitwise reproducible (the
+// reference's launcher adds with atomics, in no fixed order). Lane l holds
+// columns 4l + 256j, j < kColChunks (dim <= 1024 per pass, looping above).
+// Ids at or past rows_in_table are skipped. VEC: dim % 4 == 0 and 16-byte
+// aligned grad_out and grad_table.
+// Cost: the scans read about n^2/2 ids in all, 256 per step of a workgroup
+// (L2 hits); an id repeated r times costs its owner about
+// r / (4 * kRowsInFlight) load latencies. Meant for the GPT-2 step's
+// sequences (up to a few thousand positions).
+constexpr int kRowsInFlight = 8;
+constexpr int kColChunks = 4;
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void embed_bwd_kernel(const uint32_t *__restrict__ idx,
                                                         const float *__restrict__ grad_out,
                                                         float *__restrict__ grad_table, int n_rows, int dim,
                                                         uint32_t rows_in_table) {
+  __shared__ float4 part[4][kColChunks][64];
   const int p = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint32_t id = idx[p];
-  if (id >= rows_in_table) return;
-  // Is p the first position with this id? (Every wave scans; the answer is
-  // the same for all.)
-  for (int base = 0; base < p; base += 64) {
+  if (id >= rows_in_table) return;  // the same for the whole workgroup
+  bool found = false;
+  for (int base = w * 64; base < p && !found; base += 256) {
     const int q = base + lane;
-    const bool hit = q < p && idx[q] == id;
-    if (__any(hit)) return;
+    found = __any(q < p && idx[q] == id);
   }
-  for (int c0 = 0; c0 < dim; c0 += 4 * 256) {
-    const int c = c0 + 4 * tid;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto add_row = [&](int q) {
-      const float *g = grad_out + (size_t)q * dim;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (c + j < dim) (&acc.x)[j] += g[c + j];
-    };
-    add_row(p);
-    for (int base = p + 1; base < n_rows; base += 64) {
-      const int q = base + lane;
-      unsigned long long hits = __ballot(q < n_rows && idx[q] == id);
-      while (hits) {
-        const int b = __builtin_ctzll(hits);
-        hits &= hits - 1;
-        add_row(base + b);
-      }
-    }
-    float *dst = grad_table + (size_t)id * dim;
+  if (__syncthreads_or(found)) return;
+
+  auto load4 = [&](const float *row, int c) {
+    if (VEC) return c < dim ? *reinterpret_cast<const float4 *>(row + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (c + j < dim) dst[c + j] += (&acc.x)[j];
+      if (c + j < dim) (&r.x)[j] = row[c + j];
+    return r;
+  };
+  const int b0 = p >> 6;
+  const int first = b0 + (((w - b0) % 4) + 4) % 4;  // this wave's first block at or after p's
+  for (int c0 = 0; c0 < dim; c0 += 256 * kColChunks) {
+    float4 acc[kColChunks];
+#pragma unroll
+    for (int k = 0; k < kColChunks; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int b = first; b * 64 < n_rows; b += 4) {
+      const int q = b * 64 + lane;
+      unsigned long long hits = __ballot(q >= p && q < n_rows && idx[q] == id);
+      while (hits) {
+        int rows[kRowsInFlight], n = 0;
+        for (; hits && n < kRowsInFlight; ++n) {
+          rows[n] = b * 64 + __builtin_ctzll(hits);
+          hits &= hits - 1;
+        }
+        float4 r[kRowsInFlight][kColChunks];
+#pragma unroll
+        for (int j = 0; j < kRowsInFlight; ++j)
+#pragma unroll
+          for (int k = 0; k < kColChunks; ++k)
+            if (j < n) r[j][k] = load4(grad_out + (size_t)rows[j] * dim, c0 + 256 * k + 4 * lane);
+#pragma unroll
+        for (int j = 0; j < kRowsInFlight; ++j)
+#pragma unroll
+          for (int k = 0; k < kColChunks; ++k)
+            if (j < n) {
+              acc[k].x += r[j][k].x;
+              acc[k].y += r[j][k].y;
+              acc[k].z += r[j][k].z;
+              acc[k].w += r[j][k].w;
+            }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kColChunks; ++k) part[w][k][lane] = acc[k];
+    __syncthreads();
+    if (w == 0) {
+      float *dst = grad_table + (size_t)id * dim;
+#pragma unroll
+      for (int k = 0; k < kColChunks; ++k) {
+        const int c = c0 + 256 * k + 4 * lane;
+        float4 t = part[0][k][lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) {
+          const float4 u = part[v][k][lane];
+          t.x += u.x;
+          t.y += u.y;
+          t.z += u.z;
+          t.w += u.w;
+        }
+        if (VEC) {
+          if (c < dim) {
+            float4 d = *reinterpret_cast<float4 *>(dst + c);
+            d.x += t.x;
+            d.y += t.y;
+            d.z += t.z;
+            d.w += t.w;
+            *reinterpret_cast<float4 *>(dst + c) = d;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (c + j < dim) dst[c + j] += (&t.x)[j];
+        }
+      }
+    }
+    __syncthreads();  // part is written again by the next pass
   }
 }
 
@@ -370,8 +436,12 @@ extern "C" int dfgpt2_embedding_backward(const uint32_t *indices, const float *g
   if (n_rows == 0) return DFATTN_OK;
   if (int st = need(fn, {indices, grad_out, grad_table}); st != DFATTN_OK) return st;
   if (int st = dims_ok(fn, n_rows, dim); st != DFATTN_OK) return st;
-  hipLaunchKernelGGL(embed_bwd_kernel, dim3(n_rows), dim3(256), 0, stream, indices, grad_out, grad_table,
-                     (int)n_rows, (int)dim, rows_in_table);
+  if (dim % 4 == 0 && al(grad_out, 16) && al(grad_table, 16))
+    hipLaunchKernelGGL(embed_bwd_kernel<true>, dim3(n_rows), dim3(256), 0, stream, indices, grad_out, grad_table,
+                       (int)n_rows, (int)dim, rows_in_table);
+  else
+    hipLaunchKernelGGL(embed_bwd_kernel<false>, dim3(n_rows), dim3(256), 0, stream, indices, grad_out, grad_table,
+                       (int)n_rows, (int)dim, rows_in_table);
   return launched(fn);
 }
 

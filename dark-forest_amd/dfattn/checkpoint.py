@@ -120,8 +120,8 @@ def load_checkpoint(model, path) -> None:
             "exp_avg_sq": torch.from_numpy(v.copy()).view_as(w).to(w.device),
         }
     g["lr"], g["betas"], g["eps"], g["weight_decay"] = lr, (b1, b2), eps, wd
-    # A recorded step has the old hyper-parameters in its AdamW launch: drop it so the next replay
-    # records again (the engine clears its graph on load too, static_gpt2.rs:2106).
+    # A recorded step has the old hyper-parameters in its AdamW launch: drop it, and StaticGPT2.replay
+    # records the step again (the engine clears its graph on load too, static_gpt2.rs:2106).
     if hasattr(model, "_graph"):
         model._graph = None
 

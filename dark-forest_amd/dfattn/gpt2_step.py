@@ -259,9 +259,16 @@ class StaticGPT2:
         self._targets.copy_(targets)
 
     def replay(self):
-        """One captured training step on the current batch; returns the static loss tensor."""
+        """One captured training step on the current batch; returns the static loss tensor.
+
+        After load_checkpoint dropped the recorded step (its AdamW launch holds the old
+        hyper-parameters) the step is recorded again here, on the current batch and without eager
+        warm-up steps, which would train the loaded weights (the engine re-captures on its next step,
+        static_gpt2.rs:619-629). The returned tensor is then a new one."""
         if self._graph is None:
-            raise RuntimeError("StaticGPT2.replay before capture")
+            if getattr(self, "_tokens", None) is None:
+                raise RuntimeError("StaticGPT2.replay before capture")
+            self.capture(self._tokens, self._targets, warmup=0)
         self._graph.replay()
         return self._loss
 

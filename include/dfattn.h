@@ -297,7 +297,9 @@ int dfattn_bwd_main_strided(const float *lse, float *d_q, float *d_k, float *d_v
  * S = 4096 fits) return DFATTN_ERR_WORKSPACE before any HIP call. Every
  * call on one GPU uses that GPU's one array: calls that overlap on one GPU
  * (different streams, or threads) race and give wrong results; serialise
- * them. Nothing in the array needs to be cleared between calls.           */
+ * them. Nothing in the array needs to be cleared between calls. The first
+ * call on a device, which places the array, may itself run under stream
+ * capture: it enqueues nothing beyond the backward's kernels.              */
 #define DFATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
 int dfattn_bwd_noalloc(const float *q, const float *k, const float *v,
                        const float *o, const float *d_o, const float *lse,

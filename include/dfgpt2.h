@@ -94,7 +94,10 @@ int dfgpt2_logit_ce_chunk(float *logits, const uint32_t *targets, float *grad_lo
  * reference counterpart: the reference's loss is an atomic sum.                             */
 int dfgpt2_sum(const float *values, uint32_t n, float *out, int accumulate, hipStream_t stream);
 /* The embedding gather and its gradient on a stream (elementwise.cu:268, 291). Rows whose id is
- * rows_in_table or more are written as zeros (forward) or skipped (backward).              */
+ * rows_in_table or more are written as zeros (forward) or skipped (backward). The backward
+ * sums each id's rows in position order (bitwise reproducible; the reference uses atomics); its
+ * cost grows as n_rows^2 (id scans) and with the largest repeat count of one id (summed by one
+ * workgroup), so it is meant for sequences of up to a few thousand positions.               */
 int dfgpt2_embedding_forward(const uint32_t *indices, const float *table, float *out, uint32_t n_rows,
                              uint32_t dim, uint32_t rows_in_table, hipStream_t stream);
 int dfgpt2_embedding_backward(const uint32_t *indices, const float *grad_out, float *grad_table, uint32_t n_rows,

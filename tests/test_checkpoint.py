@@ -172,3 +172,32 @@ def test_safetensors_import_errors(tmp_path):
     with pytest.raises(ValueError, match="only F32"):
         C.load_gpt2_safetensors(tiny(), tmp_path / "f16")
 
+
+
+def test_load_drops_the_recorded_step_and_replay_records_it_again(tmp_path, monkeypatch):
+    """CPU stand-in for the graph: after load_checkpoint, replay() calls capture() on the stored
+    batch with no warm-up steps (which would train the loaded weights), then replays the new graph;
+    replay before any capture raises."""
+    m = trained()
+    with pytest.raises(RuntimeError, match="before capture"):
+        m.replay()
+    C.save_checkpoint(m, tmp_path / "m.ckpt")
+    calls = []
+
+    class Graph:
+        def replay(self):
+            calls.append("replay")
+
+    def fake_capture(tokens, targets, warmup=3):
+        calls.append(("capture", warmup, torch.equal(tokens, m._tokens)))
+        m._graph, m._loss = Graph(), torch.zeros(())
+        return m._loss
+
+    m._tokens, m._targets = batch(0)
+    m._graph = Graph()
+    monkeypatch.setattr(m, "capture", fake_capture)
+    C.load_checkpoint(m, tmp_path / "m.ckpt")
+    assert m._graph is None
+    m.replay()
+    m.replay()
+    assert calls == [("capture", 0, True), "replay", "replay"]

@@ -124,3 +124,36 @@ def test_captured_step_replays_match_eager_steps(device):
         assert abs(got - want[i]) <= 1e-6 * abs(want[i])
     for a, b in zip(eager.parameters(), graph.parameters()):
         assert torch.allclose(a, b, rtol=0, atol=1e-6)
+
+
+def test_replay_after_checkpoint_load_records_the_step_again(device, tmp_path):
+    """load_checkpoint drops the recorded step; the next replay records it again (the engine
+    re-captures on its next step, static_gpt2.rs:619-629, 2111) and trains from the loaded state:
+    its losses and weights are those of an eager model that loaded the same checkpoint."""
+    import torch
+
+    from dfattn import checkpoint as C
+
+    cfg = dict(vocab_size=500, d_model=128, n_heads=2, n_layers=2, d_ff=512, seq_len=256, lr=1e-3)
+    graph = StaticGPT2(**cfg, seed=5, capturable=True)
+    tokens, targets = synthetic_batch(500, 256, 17, device)
+    graph.capture(tokens, targets, warmup=2)
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    C.save_checkpoint(graph, tmp_path / "g.ckpt")
+    for _ in range(2):
+        graph.replay()  # past the checkpoint
+    C.load_checkpoint(graph, tmp_path / "g.ckpt")
+    assert graph._graph is None
+    eager = StaticGPT2(**cfg, seed=6, capturable=True)
+    C.load_checkpoint(eager, tmp_path / "g.ckpt")
+    want = [float(eager.step(tokens, targets)) for _ in range(3)]
+    for i in range(3):
+        loss = graph.replay()
+        torch.cuda.synchronize()
+        got = float(loss)
+        say(f"replay {i} after load: graph {got:.7f} eager {want[i]:.7f}")
+        assert abs(got - want[i]) <= 1e-6 * abs(want[i])
+    for a, b in zip(eager.parameters(), graph.parameters()):
+        assert torch.allclose(a, b, rtol=0, atol=1e-6)

@@ -424,3 +424,35 @@ def test_bias_gelu_is_the_bias_add_then_gelu(device, rows, cols):
     assert torch.equal(h, want_h) and torch.equal(out, want)
     close(out, torch.nn.functional.gelu(want_h, approximate="tanh"), 1e-5, 1e-6, "bias+gelu vs torch")
 
+
+
+@pytest.mark.parametrize("dim", [768, 771])
+def test_embedding_backward_sums_a_heavily_repeated_id_in_a_fixed_order(device, dim):
+    """S = 8192 with one id (a padding token) at 6000 positions and the rest random. The table row of
+    that id is, bit for bit, ((s0 + s1) + s2) + s3, where s_w is the float32 sum, in increasing
+    position, of its rows in the 64-position blocks b = w (mod 4) (the owner's four waves); the
+    other rows equal index_add within fp32 rounding. dim 771 takes the unaligned scalar path."""
+    import numpy as np
+    import torch
+
+    say(f"embedding backward S=8192 d={dim}, id 3 at 6000 positions")
+    g = torch.Generator(device="cpu").manual_seed(7)
+    vocab, seq = 5000, 8192
+    ids = torch.randint(0, vocab, (seq,), generator=g, dtype=torch.int32)
+    pad = torch.randperm(seq, generator=g)[:6000]
+    ids[pad] = 3
+    gy = torch.randn(seq, dim, generator=g)
+    base = (torch.randn(vocab, dim, generator=g) * 0.1)
+    gt = base.to(device)
+    ops.embedding_backward(ids.to(device), gy.to(device), gt)
+    torch.cuda.synchronize()
+    part = np.zeros((4, dim), np.float32)
+    for q in np.nonzero(ids.numpy() == 3)[0]:  # increasing positions
+        part[(q // 64) % 4] = part[(q // 64) % 4] + gy.numpy()[q]
+    total = ((part[0] + part[1]) + part[2]) + part[3]
+    got = gt.cpu().numpy()
+    assert np.array_equal(got[3], base.numpy()[3] + total)
+    want = base.double().index_add(0, ids.long(), gy.double())
+    keep = torch.ones(vocab, dtype=torch.bool)
+    keep[3] = False
+    close(torch.from_numpy(got)[keep].double(), want[keep], 1e-6, 1e-5, "other rows")

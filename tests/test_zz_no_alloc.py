@@ -4,8 +4,9 @@ GPU: two calls in a row (the second on a smaller shape, which reuses the array t
 filled) give dfattn_bwd's gradients bit for bit (the same kernels on the same inputs). The HIP
 runtime places the static array in device memory when the library first looks up its address,
 so the first call in a process may lower the device's free memory by the array's size; the
-second call changes no device memory figure (hipMemGetInfo). CPU: a shape whose workspace
-exceeds the array is rejected before any HIP call.
+second call changes no device memory figure (hipMemGetInfo). In a fresh child process whose first
+call is made under graph capture, the capture succeeds and its replays match dfattn_bwd. CPU: a
+shape whose workspace exceeds the array is rejected before any HIP call.
 """
 import ctypes
 
@@ -67,3 +68,21 @@ def test_noalloc_matches_dfattn_bwd_on_two_calls(device):
                 bar = 2e-3 * max(1.0, float(np.max(np.abs(w))))
                 say(f"S={seq_len} {name} vs oracle: max-abs {err:.3e} (bar {bar:.2e}), rel-L2 {rel:.2e}")
                 assert err <= bar and rel <= 1e-3
+
+
+@pytest.mark.gpu
+def test_first_call_under_graph_capture(device):
+    """A fresh process (tests/noalloc_capture_first.py) whose first dfattn_bwd_noalloc call is made
+    under torch.cuda.graph capture: the array is placed during the capture, the capture succeeds,
+    and three replays on changed inputs equal dfattn_bwd bit for bit."""
+    import os
+    import subprocess
+    import sys
+
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_first.py")
+    say("child process: first call under capture")
+    run = subprocess.run([sys.executable, "-u", script], capture_output=True, text=True, timeout=110)
+    for line in (run.stdout + run.stderr).strip().splitlines()[-12:]:
+        say(f"  {line}")
+    assert run.returncode == 0, "the child process failed"
+    assert "replay 2: dQ, dK, dV equal to dfattn_bwd" in run.stdout
