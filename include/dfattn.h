@@ -293,7 +293,7 @@ int dfattn_bwd_main_strided(const float *lse, float *d_q, float *d_k, float *d_v
  * the workspace: the workspace lives in a static device array of
  * DFATTN_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until
  * the process ends. Shapes whose dfattn_bwd_workspace_bytes() exceeds it
- * (for d_head = 64: n_heads * seq_len above about 63,000, e.g. H = 12,
+ * (for d_head = 64: n_heads * seq_len above about 63,900, e.g. H = 12,
  * S = 4096 fits) return DFATTN_ERR_WORKSPACE before any HIP call. Every
  * call on one GPU uses that GPU's one array: calls that overlap on one GPU
  * (different streams, or threads) race and give wrong results; serialise
