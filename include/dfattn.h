@@ -216,9 +216,10 @@ int dfattn_fwd_train(const float *q, const float *k, const float *v, float *o,
 /* Bytes of device workspace dfattn_bwd needs: O(n_heads * seq_len * d_head)
  * (a power-of-two dO scale per 64-row block, the row statistics -lse*log2(e)
  * and -Delta_i (Delta_i = dO_i . O_i) as the main phase's products take
- * them, and fp16 copies of the scaled Q, K, V and dO that the main phase
- * reads; 8 bytes per element of one input, 25 MB at H = 12, S = 4096,
- * D = 64).
+ * them, fp16 copies of the scaled Q, K, V and dO that the main phase
+ * reads, and the fp16 rounding residues of the first 64 rows of the scaled
+ * Q, K and dO, 24 KB per head; about 8 bytes per element of one input,
+ * 25 MB at H = 12, S = 4096, D = 64).
  * Returns 0 when the arguments are invalid.                                */
 size_t dfattn_bwd_workspace_bytes(uint32_t n_heads, uint32_t seq_len,
                                   uint32_t d_head);
