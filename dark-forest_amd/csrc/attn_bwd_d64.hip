@@ -34,6 +34,7 @@
 #include "dfattn_internal.h"
 
 #include <type_traits>
+#include <vector>
 
 namespace dfattn {
 namespace {
@@ -851,11 +852,23 @@ __device__ void dq_path(const BwdArgs &a, int head, int q_blk0, unsigned char *l
 // one item per head), so the greedy dispatcher approximates a
 // longest-processing-time schedule, and consecutive items, which the
 // dispatcher deals to different XCDs, mix both kinds.
+//
+// When the whole grid fits in `wg`, the items are also kept on the XCD of
+// their head: the dispatcher deals workgroup b to XCD b % 8, so position
+// b = 8j + x holds the j-th item of XCD x's list. XCD x takes every head
+// h < H - H%8 with h % 8 == x, and the H%8 remaining heads are each shared
+// by 8/(H%8) XCDs, item by item in merged order; each list keeps the merged
+// (cost) order. A head's fp16 copies then stay in the L2 of one or two XCDs
+// instead of being fetched into all eight. Head counts that do not divide
+// that way keep the plain order.
 constexpr int kSchedTable = 512;  // merged ranks listed in the kernel arguments when they fit
+constexpr int kWgTable = 768;     // workgroups listed one by one when the grid fits
 struct Sched {
   int n_qblocks, n_qtiles, S, causal, w_kv, w_q, r_kv, r_q;
   int use_table;
   unsigned short table[kSchedTable];  // (is dK/dV) << 15 | rank, in merged order
+  int use_wg;
+  unsigned short wg[kWgTable];  // per workgroup: (is dK/dV) << 15 | head << 11 | rank
   __host__ __device__ int cost_kv(int i) const {
     const int first_qb = causal ? i * (kKeysPerWg / kQBlock) : 0;
     return w_kv * max(n_qblocks - first_qb, 0);
@@ -890,20 +903,28 @@ __global__ __launch_bounds__(kThreads) void bwd_main_kernel(BwdArgs a, Sched sch
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
   const int b = blockIdx.x;
   bool kv_item;
-  int rank;
-  if (sched.use_table) {
-    const unsigned t = sched.table[b / a.H];
+  int rank, head;
+  if (sched.use_wg) {
+    const unsigned t = sched.wg[b];
     kv_item = (t >> 15) != 0;
-    rank = (int)(t & 0x7fff);
+    head = (int)((t >> 11) & 15);
+    rank = (int)(t & 0x7ff);
   } else {
-    sched.pick(b / a.H, kv_item, rank);
+    head = b % a.H;
+    if (sched.use_table) {
+      const unsigned t = sched.table[b / a.H];
+      kv_item = (t >> 15) != 0;
+      rank = (int)(t & 0x7fff);
+    } else {
+      sched.pick(b / a.H, kv_item, rank);
+    }
   }
   // The item is the same for the whole workgroup; saying so keeps every
   // address and buffer descriptor derived from it in scalar registers (the
   // table entry arrives through a vector load).
   rank = __builtin_amdgcn_readfirstlane(rank);
+  head = __builtin_amdgcn_readfirstlane(head);
   kv_item = __builtin_amdgcn_readfirstlane(kv_item ? 1 : 0) != 0;
-  const int head = b % a.H;
   if (kv_item) {
     dkdv_path(a, head, rank * kKeysPerWg, lds_raw);
   } else {
@@ -940,6 +961,31 @@ hipError_t launch_bwd_pre_d64(const float *q, const float *k, const float *v, co
                      seq_len, scale * kLog2e,
                      qkv_saved ? 0 : 1, ldi > 0 ? ldi : n_heads * kD);
   return hipGetLastError();
+}
+
+// Fills sched.wg with the XCD-local order (see Sched) from the merged table;
+// leaves use_wg = 0 when the grid or the head count does not allow it.
+void build_xcd_order(Sched &sched, int n_heads) {
+  constexpr int kXcds = 8;
+  sched.use_wg = 0;
+  const int per = sched.r_kv + sched.r_q;  // items per head
+  const int n = n_heads * per;
+  const int rest = n_heads % kXcds, full = n_heads - rest;
+  const int share = rest ? kXcds / rest : 1;  // XCDs per remaining head
+  if (!sched.use_table || n > kWgTable || n_heads > 16 || sched.r_kv > 0x7ff || sched.r_q > 0x7ff) return;
+  if (rest && (kXcds % rest != 0 || per % share != 0)) return;
+  std::vector<unsigned short> lists[kXcds];
+  for (int k = 0; k < per; ++k) {
+    const unsigned t = sched.table[k];
+    for (int h = 0; h < n_heads; ++h) {
+      const int x = h < full ? h % kXcds : (h - full) * share + k % share;
+      lists[x].push_back((unsigned short)((t & 0x8000u) | ((unsigned)h << 11) | (t & 0x7ffu)));
+    }
+  }
+  for (const auto &l : lists)
+    if ((int)l.size() * kXcds != n) return;
+  for (int b = 0; b < n; ++b) sched.wg[b] = lists[b % kXcds][b / kXcds];
+  sched.use_wg = 1;
 }
 
 hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *d_v, const void *workspace,
@@ -983,6 +1029,7 @@ hipError_t launch_bwd_main_d64(const float *lse, float *d_q, float *d_k, float *
     if (sched.use_table && k < sched.r_kv + sched.r_q) sched.pick(k, kv, rank);
     sched.table[k] = (unsigned short)((kv ? 0x8000u : 0u) | (unsigned)rank);
   }
+  build_xcd_order(sched, n_heads);
   const unsigned n_items = (unsigned)(n_heads * (sched.r_kv + sched.r_q));
   hipLaunchKernelGGL(bwd_main_kernel, dim3(n_items), dim3(kThreads), 0, stream, a, sched);
   return hipGetLastError();

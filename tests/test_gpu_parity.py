@@ -162,6 +162,18 @@ def test_long_ragged_seq_len(device, seq_len, n_heads, causal):
             want, scaled=True)
 
 
+@pytest.mark.parametrize("n_heads", [1, 2, 4, 8, 16, 24])
+def test_backward_head_counts_of_the_xcd_order(device, n_heads):
+    """S = 1024 (16 items per head): the backward main kernel lists every workgroup, keeping each
+    head's items on one XCD (8 and 16 heads: one and two heads per XCD), or sharing a head among
+    2, 4 or 8 XCDs (4, 2, 1 heads), or 3 heads per XCD (24); every item must be computed exactly
+    once. The training pair against the oracle."""
+    say(f"xcd order H={n_heads} S=1024")
+    x = O.seeded_inputs(1024, n_heads, 64, 9100 + n_heads)
+    compare(f"H={n_heads}", run_training_pair(x, n_heads, 0.125, True, device),
+            oracle_fwd_bwd(x, n_heads, 0.125, True), scaled=True)
+
+
 @pytest.mark.parametrize("d_head,n_heads", [(3, 2), (32, 4), (100, 2), (128, 2)])
 def test_generic_head_dims(device, d_head, n_heads):
     say(f"generic D={d_head} H={n_heads} S=77")
