@@ -34,7 +34,6 @@
 #include "dfattn_internal.h"
 
 #include <type_traits>
-#include <vector>
 
 namespace dfattn {
 namespace {
@@ -974,16 +973,18 @@ void build_xcd_order(Sched &sched, int n_heads) {
   const int share = rest ? kXcds / rest : 1;  // XCDs per remaining head
   if (!sched.use_table || n > kWgTable || n_heads > 16 || sched.r_kv > 0x7ff || sched.r_q > 0x7ff) return;
   if (rest && (kXcds % rest != 0 || per % share != 0)) return;
-  std::vector<unsigned short> lists[kXcds];
+  // Per-XCD lists on the stack (no host allocation per launch).
+  unsigned short lists[kXcds][kWgTable];
+  int len[kXcds] = {};
   for (int k = 0; k < per; ++k) {
     const unsigned t = sched.table[k];
     for (int h = 0; h < n_heads; ++h) {
       const int x = h < full ? h % kXcds : (h - full) * share + k % share;
-      lists[x].push_back((unsigned short)((t & 0x8000u) | ((unsigned)h << 11) | (t & 0x7ffu)));
+      lists[x][len[x]++] = (unsigned short)((t & 0x8000u) | ((unsigned)h << 11) | (t & 0x7ffu));
     }
   }
-  for (const auto &l : lists)
-    if ((int)l.size() * kXcds != n) return;
+  for (int x = 0; x < kXcds; ++x)
+    if (len[x] * kXcds != n) return;
   for (int b = 0; b < n; ++b) sched.wg[b] = lists[b % kXcds][b / kXcds];
   sched.use_wg = 1;
 }
