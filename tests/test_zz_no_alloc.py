@@ -33,6 +33,18 @@ def test_rejects_shapes_beyond_the_static_scratch():
     lib.dfattn_clear_error()
 
 
+def test_static_scratch_boundary_at_twelve_heads():
+    """H = 12: S = 5329 is the longest sequence whose workspace fits the 32 MiB array; S = 5330 is
+    rejected with DFATTN_ERR_WORKSPACE before any HIP call (the pointers are never dereferenced)."""
+    lib = dfattn.lib()
+    fits = lib.dfattn_bwd_workspace_bytes(12, 5329, 64)
+    over = lib.dfattn_bwd_workspace_bytes(12, 5330, 64)
+    assert fits <= dfattn.NOALLOC_SCRATCH_BYTES < over
+    fake = ctypes.c_void_p(0x10000)
+    assert lib.dfattn_bwd_noalloc(*([fake] * 9), 12, 5330, 64, 0.125, 1, None) == -6
+    lib.dfattn_clear_error()
+
+
 @pytest.mark.gpu
 def test_noalloc_matches_dfattn_bwd_on_two_calls(device):
     import torch
